@@ -1,0 +1,87 @@
+"""Build libflash_hog_hip.so (the C-ABI kernel library) for gfx950 with hipcc.
+
+Usage: python flash-hog_amd/build.py [--jobs N] [--out DIR]
+
+Each .hip source under csrc/ is compiled to an object in parallel, then the
+objects are linked into flash_hog/_lib/libflash_hog_hip.so next to the Python
+package that loads it. hipcc cross-compiles without a GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import pathlib
+import shutil
+import subprocess
+import sys
+
+HERE = pathlib.Path(__file__).resolve().parent
+REPO = HERE.parent
+CSRC = HERE / "csrc"
+LIB_DIR = HERE / "flash_hog" / "_lib"
+LIB_NAME = "libflash_hog_hip.so"
+ARCH = "gfx950"
+
+# -packed-fp32-ops: hipcc may not emit v_pk_{add,mul,fma}_f32; ordinary scalar
+# float code is compiled to unpacked VALU instructions.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++20",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{REPO / 'include'}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(exe):
+        raise RuntimeError("hipcc not found (expected under /opt/rocm/bin)")
+    return exe
+
+
+def _compile(src: pathlib.Path, obj: pathlib.Path) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
+
+
+def build(jobs: int | None = None, out_dir: pathlib.Path | None = None) -> pathlib.Path:
+    out_dir = pathlib.Path(out_dir) if out_dir else LIB_DIR
+    obj_dir = HERE / "_build"
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    out_dir.mkdir(parents=True, exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no .hip sources under {CSRC}")
+    objs = [obj_dir / (s.stem + ".o") for s in sources]
+    jobs = jobs or min(len(sources), os.cpu_count() or 4, 8)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_compile, sources, objs))
+    lib = out_dir / LIB_NAME
+    tmp = out_dir / (LIB_NAME + ".tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, lib)
+    return lib
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--out", type=pathlib.Path, default=None)
+    args = ap.parse_args(argv)
+    lib = build(args.jobs, args.out)
+    print(lib)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,178 @@
+// C-ABI entry points: argument validation and dispatch to the templated
+// launchers. Error reporting follows the reference's FFI handler
+// (flash_hog/csrc/tk_bwdbwd/ffi.cu:35-39, 74-76): invalid shapes are rejected
+// before anything is enqueued, launch failures are reported with the runtime's
+// message. Messages are kept per thread; there is no other global state.
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "flash_hog.h"
+#include "fhog_params.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int ok() {
+  g_last_error[0] = '\0';
+  return FHOG_OK;
+}
+
+// Tensors are read with 16-byte vector loads; fp32 row statistics with scalar loads.
+bool aligned(const void* p, uintptr_t bytes) {
+  return p != nullptr && (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
+}
+
+struct Shape {
+  int batch, n_q, n_k, heads, kv_heads, head_dim, dtype;
+  float scale;
+};
+
+int check_shape(const Shape& s, const char* who) {
+  if (!(s.scale == s.scale) || s.scale - s.scale != 0.0f)
+    return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: scale must be finite", who);
+  if (s.batch < 1 || s.n_q < 1 || s.n_k < 1 || s.heads < 1 || s.kv_heads < 1)
+    return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: sizes must be >= 1 (batch=%d n_q=%d n_k=%d heads=%d kv_heads=%d)",
+                who, s.batch, s.n_q, s.n_k, s.heads, s.kv_heads);
+  if (s.dtype != FHOG_DTYPE_F32 && s.dtype != FHOG_DTYPE_F16 && s.dtype != FHOG_DTYPE_BF16)
+    return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: unknown dtype %d", who, s.dtype);
+  if (s.head_dim < 1)
+    return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: head_dim must be >= 1, got %d", who, s.head_dim);
+  if (s.heads % s.kv_heads != 0)
+    return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: heads (%d) must be a multiple of kv_heads (%d)", who, s.heads,
+                s.kv_heads);
+  if (s.heads != s.kv_heads)
+    return fail(FHOG_ERR_UNSUPPORTED, "%s: grouped-query attention (heads=%d, kv_heads=%d) is not supported", who,
+                s.heads, s.kv_heads);
+  if (s.head_dim != 64 && s.head_dim != 128)
+    return fail(FHOG_ERR_UNSUPPORTED, "%s: head_dim must be 64 or 128, got %d", who, s.head_dim);
+  if (s.dtype == FHOG_DTYPE_F32 && s.head_dim != 64)
+    return fail(FHOG_ERR_UNSUPPORTED, "%s: fp32 supports head_dim 64 only, got %d", who, s.head_dim);
+  const long long rows = (long long)s.batch * s.heads * (s.n_q > s.n_k ? s.n_q : s.n_k);
+  if (rows * s.head_dim >= (1ll << 40) || (long long)s.batch * s.heads * ((s.n_q > s.n_k ? s.n_q : s.n_k) + 31) / 32 >= (1ll << 31))
+    return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: problem too large", who);
+  return FHOG_OK;
+}
+
+int check_ptrs(const char* who, std::initializer_list<std::pair<const char*, const void*>> tensors,
+               std::initializer_list<std::pair<const char*, const void*>> row_stats) {
+  for (const auto& p : tensors)
+    if (!aligned(p.second, 16))
+      return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: %s is null or not 16-byte aligned", who, p.first);
+  for (const auto& p : row_stats)
+    if (!aligned(p.second, 4))
+      return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: %s is null or not 4-byte aligned", who, p.first);
+  return FHOG_OK;
+}
+
+int launch_status(hipError_t e, const char* who) {
+  if (e != hipSuccess) return fail(FHOG_ERR_LAUNCH, "%s: %s", who, hipGetErrorString(e));
+  return ok();
+}
+
+// Calls f.template operator()<T, D, CAUSAL>() for the runtime (dtype, head_dim, causal).
+template <typename F>
+hipError_t dispatch(int dtype, int head_dim, bool causal, F&& f) {
+#define FHOG_CASE(T, D)                                          \
+  return causal ? f.template operator()<T, D, true>() : f.template operator()<T, D, false>();
+  if (dtype == FHOG_DTYPE_BF16) {
+    if (head_dim == 64) { FHOG_CASE(__bf16, 64) }
+    FHOG_CASE(__bf16, 128)
+  }
+  if (dtype == FHOG_DTYPE_F16) {
+    if (head_dim == 64) { FHOG_CASE(_Float16, 64) }
+    FHOG_CASE(_Float16, 128)
+  }
+  FHOG_CASE(float, 64)
+#undef FHOG_CASE
+}
+
+}  // namespace
+
+extern "C" {
+
+int fhog_abi_version(void) { return 100; }
+
+const char* fhog_status_string(int status) {
+  switch (status) {
+    case FHOG_OK: return "ok";
+    case FHOG_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case FHOG_ERR_UNSUPPORTED: return "unsupported";
+    case FHOG_ERR_LAUNCH: return "kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+const char* fhog_last_error(void) { return g_last_error; }
+
+size_t fhog_row_stat_bytes(int batch, int heads, int n_q) {
+  if (batch < 1 || heads < 1 || n_q < 1) return 0;
+  return (size_t)batch * heads * n_q * sizeof(float);
+}
+
+int fhog_attention_fwd(fhog_stream_t stream, const void* q, const void* k, const void* v, void* o, float* lse,
+                       int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim, int dtype, int causal,
+                       float scale) {
+  static const char* who = "fhog_attention_fwd";
+  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, scale};
+  if (int st = check_shape(s, who)) return st;
+  if (int st = check_ptrs(who, {{"q", q}, {"k", k}, {"v", v}, {"o", o}}, {{"lse", lse}})) return st;
+  auto run = [&]<typename T, int D, bool C>() {
+    fhog::FwdParams<T> p{(const T*)q, (const T*)k, (const T*)v, (T*)o, lse, batch, n_q, n_k, heads, scale};
+    return fhog::launch_fwd<T, D, C>(p, (hipStream_t)stream);
+  };
+  return launch_status(dispatch(dtype, head_dim, causal != 0, run), who);
+}
+
+int fhog_attention_bwd(fhog_stream_t stream, const void* q, const void* k, const void* v, const void* o,
+                       const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta, int batch,
+                       int n_q, int n_k, int heads, int kv_heads, int head_dim, int dtype, int causal, float scale) {
+  static const char* who = "fhog_attention_bwd";
+  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, scale};
+  if (int st = check_shape(s, who)) return st;
+  if (int st = check_ptrs(who, {{"q", q}, {"k", k}, {"v", v}, {"o", o}, {"dout", dout}, {"dq", dq}, {"dk", dk},
+                                {"dv", dv}},
+                           {{"lse", lse}, {"delta", delta}}))
+    return st;
+  auto run = [&]<typename T, int D, bool C>() {
+    fhog::BwdParams<T> p{(const T*)q, (const T*)k, (const T*)v, (const T*)o, (const T*)dout, lse,
+                         (T*)dq, (T*)dk, (T*)dv, delta, batch, n_q, n_k, heads, scale};
+    return fhog::launch_bwd<T, D, C>(p, (hipStream_t)stream);
+  };
+  return launch_status(dispatch(dtype, head_dim, causal != 0, run), who);
+}
+
+int fhog_attention_bwdbwd(fhog_stream_t stream, const void* q, const void* k, const void* v, const void* o,
+                          const void* dout, const void* ddq, const void* ddk, const void* ddv, const float* lse,
+                          void* dq2, void* dk2, void* dv2, void* ddo, float* delta, float* ddelta, float* bstat,
+                          int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim, int dtype, int causal,
+                          float scale) {
+  static const char* who = "fhog_attention_bwdbwd";
+  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, scale};
+  if (int st = check_shape(s, who)) return st;
+  if (int st = check_ptrs(who, {{"q", q}, {"k", k}, {"v", v}, {"o", o}, {"dout", dout}, {"ddq", ddq},
+                                {"ddk", ddk}, {"ddv", ddv}, {"dq2", dq2}, {"dk2", dk2}, {"dv2", dv2},
+                                {"ddo", ddo}},
+                           {{"lse", lse}, {"delta", delta}, {"ddelta", ddelta}, {"bstat", bstat}}))
+    return st;
+  auto run = [&]<typename T, int D, bool C>() {
+    fhog::BwdBwdParams<T> p{(const T*)q,   (const T*)k,   (const T*)v,   (const T*)o, (const T*)dout,
+                            (const T*)ddq, (const T*)ddk, (const T*)ddv, lse,         (T*)dq2,
+                            (T*)dk2,       (T*)dv2,       (T*)ddo,       delta,       ddelta,
+                            bstat,         batch,         n_q,           n_k,         heads,
+                            scale};
+    return fhog::launch_bwdbwd<T, D, C>(p, (hipStream_t)stream);
+  };
+  return launch_status(dispatch(dtype, head_dim, causal != 0, run), who);
+}
+
+}  // extern "C"

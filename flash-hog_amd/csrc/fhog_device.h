@@ -1,0 +1,198 @@
+// Device-side building blocks shared by every Flash-HOG kernel on gfx950.
+//
+// All kernels work on one 64-lane wavefront per 32-row slab and use the CDNA
+// 32x32x16 matrix instruction (v_mfma_f32_32x32x16_{bf16,f16}); fp32 inputs use
+// eight v_mfma_f32_32x32x2f32 per 16-deep step so that one code path serves all
+// three dtypes.
+//
+// Operand layouts of the 32x32x16 instruction (lane l, n = l & 31, g = l >> 5):
+//   A (32 x 16):  lane holds A[m = n][k = 8g + e],          e = 0..7
+//   B (16 x 32):  lane holds B[k = 8g + e][n],              e = 0..7
+//   C (32 x 32):  lane holds C[m = 8(r/4) + 4g + r%4][n],    r = 0..15
+// Because a C tile is indexed by the lane along n, a C tile converted to the
+// input dtype can be fed straight back as an A or B operand for a product that
+// contracts over its m index. Register r = 8s + e of step s then stands for
+// m = cperm(s, g, e) = 16s + 8(e/4) + 4g + e%4; the other operand is read from
+// LDS with the same permutation (two 4-element runs per lane).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fhog {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+template <typename T> struct Vec;
+template <> struct Vec<__bf16> { typedef bf16x8 x8; typedef bf16x4 x4; };
+template <> struct Vec<_Float16> { typedef f16x8 x8; typedef f16x4 x4; };
+template <> struct Vec<float> { typedef f32x8 x8; typedef f32x4 x4; };
+
+template <typename T> using V8 = typename Vec<T>::x8;
+template <typename T> using V4 = typename Vec<T>::x4;
+
+// C += A * B on a 32x32 tile with a 16-deep contraction.
+template <typename T> __device__ __forceinline__ f32x16 mma(V8<T> a, V8<T> b, f32x16 c);
+
+template <> __device__ __forceinline__ f32x16 mma<__bf16>(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ f32x16 mma<_Float16>(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+// fp32: instruction e contracts over lane groups g = 0, 1, i.e. logical k = 8g + e.
+template <> __device__ __forceinline__ f32x16 mma<float>(f32x8 a, f32x8 b, f32x16 c) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], b[e], c, 0, 0, 0);
+  return c;
+}
+
+template <typename T> __device__ __forceinline__ V8<T> cvt8(f32x8 x) {
+  return __builtin_convertvector(x, V8<T>);
+}
+template <typename T> __device__ __forceinline__ V4<T> cvt4(f32x4 x) {
+  return __builtin_convertvector(x, V4<T>);
+}
+
+__device__ __forceinline__ f32x8 lo8(f32x16 x) {
+  return __builtin_shufflevector(x, x, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+__device__ __forceinline__ f32x8 hi8(f32x16 x) {
+  return __builtin_shufflevector(x, x, 8, 9, 10, 11, 12, 13, 14, 15);
+}
+
+template <typename T> __device__ __forceinline__ V8<T> zero8() {
+  V8<T> z;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) z[e] = (T)0.0f;
+  return z;
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) z[r] = 0.0f;
+  return z;
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Sum of a lane value with the lane 32 positions away (the other row group of
+// a 32x32 tile).
+__device__ __forceinline__ float xgroup_sum(float x) { return x + __shfl_xor(x, 32, 64); }
+__device__ __forceinline__ float xgroup_max(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
+
+// ---------------------------------------------------------------------------
+// Tiles of 32 rows x D columns staged through LDS.
+//
+// A wave moves one such tile: lane (kq = l / 8, c = l % 8) owns rows 4kq..4kq+3
+// and the 8-column chunk c (plus 8 * pass for D > 64). LDS holds the tile twice:
+// row-major with a padded stride RS (for operands that contract over columns),
+// and transposed (column-major) with a padded stride TS (for operands that
+// contract over rows).
+// ---------------------------------------------------------------------------
+// Padding: a row-major row is D + 8 elements, so consecutive rows start 4
+// banks apart for 2-byte types (8 lanes of a 16-byte read are conflict free);
+// a transposed row is 36 elements, so the 8-byte (16-byte for fp32) reads of
+// 16 consecutive columns land on distinct banks.
+template <typename T, int D> struct TileGeom {
+  static constexpr int kRows = 32;
+  static constexpr int kPasses = D / 64;
+  static constexpr int RS = D + 8;
+  static constexpr int TS = kRows + 4;
+  static constexpr int kRowElems = kRows * RS;
+  static constexpr int kTrElems = D * TS;
+};
+
+template <typename T, int D> struct TileRegs {
+  V8<T> r[TileGeom<T, D>::kPasses][4];
+};
+
+// Load a 32 x D tile whose row i lives at base + i * row_stride; rows at or
+// beyond nvalid are zero-filled.
+template <typename T, int D>
+__device__ __forceinline__ void tile_load(TileRegs<T, D>& t, const T* __restrict__ base,
+                                          long row_stride, int nvalid, int lane) {
+  const int kq = lane >> 3, c = lane & 7;
+#pragma unroll
+  for (int p = 0; p < TileGeom<T, D>::kPasses; ++p) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 4 * kq + j;
+      const int col = 8 * (c + 8 * p);
+      if (row < nvalid)
+        t.r[p][j] = *reinterpret_cast<const V8<T>*>(base + (long)row * row_stride + col);
+      else
+        t.r[p][j] = zero8<T>();
+    }
+  }
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void tile_store_lds(const TileRegs<T, D>& t, T* __restrict__ row_major,
+                                               T* __restrict__ transposed, int lane) {
+  typedef TileGeom<T, D> G;
+  const int kq = lane >> 3, c = lane & 7;
+#pragma unroll
+  for (int p = 0; p < G::kPasses; ++p) {
+    const int col = 8 * (c + 8 * p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<V8<T>*>(row_major + (4 * kq + j) * G::RS + col) = t.r[p][j];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      V4<T> w;
+      w[0] = t.r[p][0][e];
+      w[1] = t.r[p][1][e];
+      w[2] = t.r[p][2][e];
+      w[3] = t.r[p][3][e];
+      *reinterpret_cast<V4<T>*>(transposed + (col + e) * G::TS + 4 * kq) = w;
+    }
+  }
+}
+
+// Operand for a product contracting over columns (the head dimension): lane
+// (n, g) reads row n, columns 16 ks + 8g .. +7.
+template <typename T, int D>
+__device__ __forceinline__ V8<T> frag_row(const T* __restrict__ row_major, int n, int g, int ks) {
+  return *reinterpret_cast<const V8<T>*>(row_major + n * TileGeom<T, D>::RS + 16 * ks + 8 * g);
+}
+
+// Operand for a product contracting over the 32 tile rows, in the permuted
+// order of a C tile fed back as an operand: lane (n, g) reads column `col`,
+// rows cperm(s, g, 0..7).
+template <typename T, int D>
+__device__ __forceinline__ V8<T> frag_tr(const T* __restrict__ transposed, int col, int g, int s) {
+  const T* p = transposed + col * TileGeom<T, D>::TS + 16 * s + 4 * g;
+  V4<T> a = *reinterpret_cast<const V4<T>*>(p);
+  V4<T> b = *reinterpret_cast<const V4<T>*>(p + 8);
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Row index (within a 32-row C tile) held by register r of a lane in group g.
+__device__ __forceinline__ int crow(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+// ---------------------------------------------------------------------------
+// Grid mapping. Workgroups are dispatched round-robin over the 8 XCDs of an
+// MI355X, each with its own L2. Blocks that read the same (batch, head) stream
+// are therefore remapped onto one XCD, in order, so that their shared K/V (or
+// Q/dO) tiles hit that XCD's L2.
+// ---------------------------------------------------------------------------
+constexpr int kNumXcd = 8;
+
+__device__ __forceinline__ int xcd_remap(int id, int total) {
+  const int per = total / kNumXcd;
+  if (id >= per * kNumXcd) return id;
+  return (id % kNumXcd) * per + id / kNumXcd;
+}
+
+}  // namespace fhog

@@ -1,0 +1,43 @@
+// Launch parameter blocks and launcher declarations shared by the kernel files
+// and the C-ABI translation unit.
+//
+// Tensors are BTNH (batch, tokens, heads, head_dim) and contiguous, the layout
+// of the reference's attention seam; row statistics are (batch, heads, tokens)
+// fp32, the layout of the reference's logsumexp residual.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace fhog {
+
+template <typename T> struct FwdParams {
+  const T* q; const T* k; const T* v;
+  T* o; float* lse;
+  int batch, nq, nk, heads;
+  float scale;
+};
+
+template <typename T> struct BwdParams {
+  const T* q; const T* k; const T* v; const T* o; const T* dout;
+  const float* lse;
+  T* dq; T* dk; T* dv;
+  float* delta;
+  int batch, nq, nk, heads;
+  float scale;
+};
+
+template <typename T> struct BwdBwdParams {
+  const T* q; const T* k; const T* v; const T* o; const T* dout;
+  const T* ddq; const T* ddk; const T* ddv;
+  const float* lse;
+  T* dq2; T* dk2; T* dv2; T* ddo;
+  float* delta; float* ddelta; float* bstat;
+  int batch, nq, nk, heads;
+  float scale;
+};
+
+template <typename T, int D, bool CAUSAL> hipError_t launch_fwd(const FwdParams<T>& p, hipStream_t s);
+template <typename T, int D, bool CAUSAL> hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t s);
+template <typename T, int D, bool CAUSAL> hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t s);
+
+}  // namespace fhog

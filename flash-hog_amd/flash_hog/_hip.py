@@ -1,0 +1,185 @@
+"""ctypes binding of libflash_hog_hip.so, the C ABI declared in include/flash_hog.h.
+
+This mirrors the plugin loader of the reference's native path
+(flash_hog/jax/_tk_gpu.py:26-58): the library path comes from the
+FLASH_HOG_HIP_LIB environment variable or the in-tree build, the library is
+loaded once, and a missing library is an error (there is no fallback path).
+
+The torch-level helpers below take device tensors, check them, allocate the
+outputs and the fp32 row-statistic workspace with torch's caching allocator,
+and enqueue the kernels on torch's current stream for the tensors' device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import os
+import pathlib
+
+import torch
+
+LIB_ENV = "FLASH_HOG_HIP_LIB"
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "_lib" / "libflash_hog_hip.so"
+
+FHOG_OK = 0
+FHOG_ERR_INVALID_ARGUMENT = 1
+FHOG_ERR_UNSUPPORTED = 2
+FHOG_ERR_LAUNCH = 3
+
+DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+
+SIGNATURES = {
+    "fhog_abi_version": (_i, []),
+    "fhog_status_string": (ctypes.c_char_p, [_i]),
+    "fhog_last_error": (ctypes.c_char_p, []),
+    "fhog_row_stat_bytes": (ctypes.c_size_t, [_i, _i, _i]),
+    "fhog_attention_fwd": (_i, [_p, _p, _p, _p, _p, _p] + [_i] * 8 + [_f]),
+    "fhog_attention_bwd": (_i, [_p] * 11 + [_i] * 8 + [_f]),
+    "fhog_attention_bwdbwd": (_i, [_p] * 17 + [_i] * 8 + [_f]),
+}
+
+
+class FlashHogError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+def library_path() -> pathlib.Path:
+    return pathlib.Path(os.environ.get(LIB_ENV) or LIB_PATH)
+
+
+@functools.cache
+def lib() -> ctypes.CDLL:
+    path = library_path()
+    if not path.exists():
+        raise ImportError(
+            f"Flash-HOG HIP library not found at {path}; build it with "
+            f"`python flash-hog_amd/build.py` (or set {LIB_ENV})")
+    handle = ctypes.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    return handle
+
+
+def check(status: int) -> None:
+    if status != FHOG_OK:
+        L = lib()
+        msg = L.fhog_last_error().decode() or L.fhog_status_string(status).decode()
+        raise FlashHogError(status, msg)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_inputs(named, dtype=None):
+    first = None
+    for name, t in named:
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if t.device.type != "cuda":
+            raise ValueError(f"{name} must be on a GPU device, got {t.device}")
+        if first is None:
+            first = t
+        if t.device != first.device:
+            raise ValueError(f"{name} is on {t.device}, expected {first.device}")
+        if dtype is not None and t.dtype != dtype:
+            raise ValueError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    return first
+
+
+def _dims(q: torch.Tensor, k: torch.Tensor):
+    if q.ndim != 4 or k.ndim != 4:
+        raise ValueError(f"expected (B, T, N, H) tensors, got q{tuple(q.shape)} k{tuple(k.shape)}")
+    B, Tq, N, Hd = q.shape
+    Bk, Tk, Nk, Hk = k.shape
+    if Bk != B or Hk != Hd:
+        raise ValueError(f"q{tuple(q.shape)} and k{tuple(k.shape)} disagree on batch or head_dim")
+    if q.dtype not in DTYPE_CODES:
+        raise ValueError(f"unsupported dtype {q.dtype}")
+    return B, Tq, Tk, N, Nk, Hd
+
+
+def _expect(name, t, shape, dtype=None):
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} has dtype {t.dtype}, expected {dtype}")
+
+
+def attention_fwd(q, k, v, causal: bool, scale: float):
+    """O (B, T, N, H) in q's dtype and the natural-log logsumexp L (B, N, T) fp32."""
+    _check_inputs([("q", q), ("k", k), ("v", v)], q.dtype)
+    B, Tq, Tk, N, Nk, Hd = _dims(q, k)
+    _expect("v", v, k.shape)
+    q, k, v = (x.contiguous() for x in (q, k, v))
+    o = torch.empty_like(q)
+    lse = torch.empty((B, N, Tq), device=q.device, dtype=torch.float32)
+    with torch.cuda.device(q.device):
+        check(lib().fhog_attention_fwd(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse),
+            B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], int(bool(causal)), float(scale)))
+    return o, lse
+
+
+def attention_bwd(q, k, v, o, dout, lse, causal: bool, scale: float):
+    """dQ, dK, dV of attention given its residual; also returns D (B, N, T) fp32."""
+    _check_inputs([("q", q), ("k", k), ("v", v), ("o", o), ("dout", dout)], q.dtype)
+    _check_inputs([("q", q), ("lse", lse)])
+    B, Tq, Tk, N, Nk, Hd = _dims(q, k)
+    _expect("v", v, k.shape)
+    _expect("o", o, q.shape)
+    _expect("dout", dout, q.shape)
+    _expect("lse", lse, (B, N, Tq), torch.float32)
+    q, k, v, o, dout, lse = (x.contiguous() for x in (q, k, v, o, dout, lse))
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    delta = torch.empty((B, N, Tq), device=q.device, dtype=torch.float32)
+    with torch.cuda.device(q.device):
+        check(lib().fhog_attention_bwd(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(dout), _ptr(lse),
+            _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta),
+            B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], int(bool(causal)), float(scale)))
+    return dq, dk, dv, delta
+
+
+def attention_bwdbwd(q, k, v, o, dout, ddq, ddk, ddv, lse, causal: bool, scale: float,
+                     return_stats: bool = False):
+    """dQ2, dK2, dV2, ddO of the double backward [and the row statistics D, dD, B]."""
+    _check_inputs([("q", q), ("k", k), ("v", v), ("o", o), ("dout", dout),
+                   ("ddq", ddq), ("ddk", ddk), ("ddv", ddv)], q.dtype)
+    _check_inputs([("q", q), ("lse", lse)])
+    B, Tq, Tk, N, Nk, Hd = _dims(q, k)
+    _expect("v", v, k.shape)
+    for name, t in (("o", o), ("dout", dout), ("ddq", ddq)):
+        _expect(name, t, q.shape)
+    for name, t in (("ddk", ddk), ("ddv", ddv)):
+        _expect(name, t, k.shape)
+    _expect("lse", lse, (B, N, Tq), torch.float32)
+    q, k, v, o, dout, ddq, ddk, ddv, lse = (
+        x.contiguous() for x in (q, k, v, o, dout, ddq, ddk, ddv, lse))
+    dq2, dk2, dv2, ddo = (torch.empty_like(x) for x in (q, k, v, dout))
+    stats = torch.empty((3, B, N, Tq), device=q.device, dtype=torch.float32)
+    with torch.cuda.device(q.device):
+        check(lib().fhog_attention_bwdbwd(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(dout),
+            _ptr(ddq), _ptr(ddk), _ptr(ddv), _ptr(lse),
+            _ptr(dq2), _ptr(dk2), _ptr(dv2), _ptr(ddo),
+            _ptr(stats[0]), _ptr(stats[1]), _ptr(stats[2]),
+            B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], int(bool(causal)), float(scale)))
+    if return_stats:
+        return dq2, dk2, dv2, ddo, (stats[0], stats[1], stats[2])
+    return dq2, dk2, dv2, ddo

@@ -1,0 +1,115 @@
+/*
+ * flash_hog.h - C ABI of the MI355X-native Flash-HOG attention kernels.
+ *
+ * Plain pointers and sizes only. Every entry point enqueues its kernels on the
+ * given HIP stream and returns without synchronising; it allocates nothing,
+ * frees nothing and keeps no pointer after it returns (all outputs and the
+ * fp32 row-statistic workspace are caller owned, as the reference's XLA FFI
+ * handler exposes its dD/B scratch as results). No entry point holds mutable
+ * global state, so concurrent calls on different streams are safe.
+ *
+ * Layouts (identical to the reference's attention seam):
+ *   q, o, dout, ddq, dq, dq2, ddo   : (batch, n_q, heads, head_dim) contiguous
+ *   k, v, ddk, ddv, dk, dv, dk2, dv2: (batch, n_k, heads, head_dim) contiguous
+ *   lse, delta, ddelta, bstat       : (batch, heads, n_q) fp32 contiguous
+ * lse is the natural-log logsumexp of the scaled, masked logits
+ * (flash_hog/jax/_pallas_gpu_kernel.py:97). Causal masking is top-left
+ * aligned: query i attends to keys j <= i (_pallas_gpu_kernel.py:37-41).
+ * Tensor pointers must be 16-byte aligned, row-statistic pointers 4-byte aligned.
+ *
+ * Supported: dtype FHOG_DTYPE_{BF16,F16} with head_dim 64 or 128,
+ * FHOG_DTYPE_F32 with head_dim 64; any n_q, n_k >= 1 (ragged tails are
+ * masked); heads == kv_heads.
+ */
+#ifndef FLASH_HOG_H_
+#define FLASH_HOG_H_
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same type as hipStream_t. */
+typedef struct ihipStream_t* fhog_stream_t;
+
+enum fhog_status {
+  FHOG_OK = 0,
+  FHOG_ERR_INVALID_ARGUMENT = 1, /* null/misaligned pointer, bad size, bad enum */
+  FHOG_ERR_UNSUPPORTED = 2,      /* valid request this build has no kernel for */
+  FHOG_ERR_LAUNCH = 3            /* the HIP runtime rejected a kernel launch */
+};
+
+enum fhog_dtype { FHOG_DTYPE_F32 = 0, FHOG_DTYPE_F16 = 1, FHOG_DTYPE_BF16 = 2 };
+
+/* Version of this ABI (major * 100 + minor). */
+int fhog_abi_version(void);
+
+/* Static description of a status code. */
+const char* fhog_status_string(int status);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fhog_last_error(void);
+
+/* Bytes of fp32 row-statistic workspace per (delta, ddelta, bstat) array:
+ * batch * heads * n_q * 4. */
+size_t fhog_row_stat_bytes(int batch, int heads, int n_q);
+
+/*
+ * Forward: o = softmax(scale q k^T [causal]) v and lse.
+ * Replaces the cuDNN forward the reference reaches through
+ * dot_product_attention_fwd / dot_product_attention_fwd_rule
+ * (flash_hog/jax/_attention_impl.py:224-239), which returns (out, activation)
+ * with activation = the (B, N, T) fp32 logsumexp.
+ */
+int fhog_attention_fwd(fhog_stream_t stream,
+                       const void* q, const void* k, const void* v,
+                       void* o, float* lse,
+                       int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim,
+                       int dtype, int causal, float scale);
+
+/*
+ * First backward: dq, dk, dv from (q, k, v, o, lse, dout).
+ * Replaces the cuDNN backward the reference reaches through
+ * dot_product_attention_bwd_rule (flash_hog/jax/_attention_impl.py:242-261).
+ * delta (caller-owned, fhog_row_stat_bytes) receives D = rowsum(o * dout).
+ */
+int fhog_attention_bwd(fhog_stream_t stream,
+                       const void* q, const void* k, const void* v,
+                       const void* o, const void* dout, const float* lse,
+                       void* dq, void* dk, void* dv, float* delta,
+                       int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim,
+                       int dtype, int causal, float scale);
+
+/*
+ * Double backward (Flash-HOG): given the residual (q, k, v, o, lse, dout) of
+ * the first backward and the cotangents (ddq, ddk, ddv) of its outputs,
+ * returns dq2, dk2, dv2 (cotangents of q, k, v) and ddo (cotangent of dout).
+ * Replaces dot_product_attention_bwd_rule_bwd_rule
+ * (flash_hog/jax/_attention_impl.py:278-303) -> flash_bwdbwd
+ * (flash_hog/jax/_pallas_gpu.py:51-114) -> flash_bwdbwd0
+ * (flash_hog/jax/_pallas_gpu_kernel.py:49-422), and the XLA FFI handler
+ * TkBwdBwd (flash_hog/csrc/tk_bwdbwd/ffi.cu:26-98), whose inputs
+ * (Q,K,V,dO,ddQ,ddK,ddV,L,D), attribute scale and results
+ * (dQ2,ddO,dK2,dV2,dD,B) it mirrors, except that D is computed here from o
+ * (as flash_bwdbwd0 does at _pallas_gpu_kernel.py:110) and written to delta.
+ * delta, ddelta, bstat: caller-owned workspace, fhog_row_stat_bytes each;
+ * on return they hold D, dD and B.
+ * Two kernels are enqueued on stream; the second reads the statistics the
+ * first writes.
+ */
+int fhog_attention_bwdbwd(fhog_stream_t stream,
+                          const void* q, const void* k, const void* v,
+                          const void* o, const void* dout,
+                          const void* ddq, const void* ddk, const void* ddv,
+                          const float* lse,
+                          void* dq2, void* dk2, void* dv2, void* ddo,
+                          float* delta, float* ddelta, float* bstat,
+                          int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim,
+                          int dtype, int causal, float scale);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASH_HOG_H_ */

@@ -1,0 +1,73 @@
+"""fp32 closed-form double backward on the GPU, one head at a time.
+
+A checker for the full-size configurations, where the numpy fp64 oracle would
+take minutes: the same equations as oracle/attention.py:bwd_bwd_head
+(flash_hog/_jax_refs/jax_impl.py:301-336), materialising (N_Q, N_K) fp32
+matrices for one (batch, head) at a time. It is pinned against the fp64 oracle
+in tests/test_gpu_parity.py::test_gpu_reference_matches_oracle.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def _mask(n_q, n_k, device):
+    return torch.arange(n_k, device=device)[None, :] <= torch.arange(n_q, device=device)[:, None]
+
+
+def bwdbwd_head(q, k, v, o, do, ddq, ddk, ddv, lse, scale, causal):
+    mm = torch.mm
+    s = mm(q, k.t().contiguous()) * scale
+    if causal:
+        s = s.masked_fill(~_mask(q.shape[0], k.shape[0], q.device), float("-inf"))
+    p = torch.exp(s - lse[:, None])
+    dp = mm(do, v.t().contiguous())
+    dds = scale * (mm(ddq, k.t().contiguous()) + mm(q, ddk.t().contiguous()))
+    d = (o * do).sum(-1)
+    dd = (dds * p).sum(-1)
+    dp2 = mm(do, ddv.t().contiguous()) - dp * dd[:, None] - dds * d[:, None] + dp * dds
+    b = (dp2 * p).sum(-1)
+    ds = scale * p * (dp - d[:, None])
+    ds2 = scale * p * (dp2 - b[:, None])
+    ddp = p * (dds - dd[:, None])
+    dq2 = mm(ds, ddk) + mm(ds2, k)
+    dk2 = mm(ds.t().contiguous(), ddq) + mm(ds2.t().contiguous(), q)
+    dv2 = mm(ddp.t().contiguous(), do)
+    ddo = mm(p, ddv) + mm(ddp, v)
+    return dq2, dk2, dv2, ddo
+
+
+def fwd_head(q, k, v, scale, causal):
+    s = torch.mm(q, k.t().contiguous()) * scale
+    if causal:
+        s = s.masked_fill(~_mask(q.shape[0], k.shape[0], q.device), float("-inf"))
+    lse = torch.logsumexp(s, dim=-1)
+    return torch.mm(torch.exp(s - lse[:, None]), v), lse
+
+
+def bwdbwd(q, k, v, o, do, ddq, ddk, ddv, lse, scale, causal):
+    """(B, T, N, H) inputs of any float dtype -> fp32 dQ2, dK2, dV2, ddO."""
+    f = lambda x: x.float()
+    q, k, v, o, do, ddq, ddk, ddv, lse = map(f, (q, k, v, o, do, ddq, ddk, ddv, lse))
+    outs = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(do)]
+    B, _, H, _ = q.shape
+    for b in range(B):
+        for h in range(H):
+            args = [x[b, :, h, :].contiguous() for x in (q, k, v, o, do, ddq, ddk, ddv)]
+            res = bwdbwd_head(*args, lse[b, h].contiguous(), scale, causal)
+            for dst, r in zip(outs, res):
+                dst[b, :, h, :] = r
+    return tuple(outs)
+
+
+def fwd(q, k, v, scale, causal):
+    q, k, v = q.float(), k.float(), v.float()
+    B, T, H, D = q.shape
+    o = torch.empty((B, T, H, v.shape[-1]), device=q.device)
+    lse = torch.empty((B, H, T), device=q.device)
+    for b in range(B):
+        for h in range(H):
+            o[b, :, h, :], lse[b, h] = fwd_head(q[b, :, h, :].contiguous(), k[b, :, h, :].contiguous(),
+                                                v[b, :, h, :].contiguous(), scale, causal)
+    return o, lse

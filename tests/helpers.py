@@ -1,0 +1,61 @@
+"""Shared input generation and comparison helpers for the test suite."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+# Per-output tolerance on max|a - r| / max|r| (the north-star parity bar):
+# fp32 runs below 1e-3; bf16/fp16 runs below 2e-2 against an fp32-or-better reference.
+TOL = {torch.float32: 1e-3, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+
+# Order in which per-tensor seeds are derived: seed + index.
+TENSOR_ORDER = ("q", "k", "v", "do", "ddq", "ddk", "ddv")
+
+
+def make_inputs(batch, n_q, n_k, heads, head_dim, dtype, seed=0, qkv_scale=1.0, device="cpu"):
+    """Seeded N(0, 1) inputs in (B, T, N, H) layout, rounded to dtype.
+
+    Tensor i of TENSOR_ORDER is drawn from torch.Generator seeded with seed + i;
+    q, k, v are multiplied by qkv_scale before rounding.
+    """
+    shapes = {"q": (batch, n_q, heads, head_dim), "do": (batch, n_q, heads, head_dim),
+              "ddq": (batch, n_q, heads, head_dim)}
+    out = {}
+    for i, name in enumerate(TENSOR_ORDER):
+        shape = shapes.get(name, (batch, n_k, heads, head_dim))
+        gen = torch.Generator().manual_seed(seed + i)
+        x = torch.randn(shape, generator=gen, dtype=torch.float32)
+        if name in ("q", "k", "v"):
+            x = x * qkv_scale
+        out[name] = x.to(dtype).to(device)
+    return out
+
+
+def rel_err(a, r, floor: float = 0.0) -> float:
+    """max|a - r| / max(max|r|, floor).
+
+    floor keeps outputs that are identically zero in exact arithmetic (for
+    example dQ of a single-token sequence, where P = 1 and dP = D) from being
+    divided by round-off: their error is then measured against floor.
+    """
+    a = torch.as_tensor(a).double().cpu()
+    r = torch.as_tensor(r).double().cpu()
+    den = max(r.abs().max().item() if r.numel() else 0.0, floor)
+    num = (a - r).abs().max().item() if r.numel() else 0.0
+    return num / den if den > 0 else num
+
+
+# Output magnitudes of the seeded N(0, 1) problems are O(1); a reference whose
+# largest entry is below this is treated as exactly zero (see rel_err).
+DEGENERATE_FLOOR = 1e-2
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)
+
+
+def to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().double().cpu().numpy()

@@ -1,0 +1,119 @@
+"""The C-ABI library loads, exports what include/flash_hog.h declares and
+rejects invalid calls before touching the GPU (no kernels run here)."""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+REPO = pathlib.Path(__file__).resolve().parent.parent
+HEADER = REPO / "include" / "flash_hog.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fhog_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from flash_hog import _hip
+
+    if not _hip.library_path().exists():
+        pytest.fail(f"{_hip.library_path()} missing: run python flash-hog_amd/build.py")
+    return _hip.lib()
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for n in ("fhog_attention_fwd", "fhog_attention_bwd", "fhog_attention_bwdbwd",
+              "fhog_last_error", "fhog_status_string", "fhog_abi_version", "fhog_row_stat_bytes"):
+        assert n in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_python_signatures_cover_the_header():
+    from flash_hog import _hip
+
+    assert set(_hip.SIGNATURES) == set(declared_functions())
+
+
+def test_status_strings(lib):
+    assert lib.fhog_abi_version() == 100
+    assert lib.fhog_status_string(0) == b"ok"
+    assert lib.fhog_status_string(1) == b"invalid argument"
+    assert lib.fhog_status_string(2) == b"unsupported"
+    assert lib.fhog_status_string(3) == b"kernel launch failed"
+    assert lib.fhog_status_string(99) == b"unknown status"
+
+
+def test_row_stat_bytes(lib):
+    assert lib.fhog_row_stat_bytes(4, 16, 2048) == 4 * 16 * 2048 * 4
+    assert lib.fhog_row_stat_bytes(0, 16, 2048) == 0
+
+
+def _bwdbwd_args(ptr=16, batch=1, n_q=16, n_k=16, heads=1, kv_heads=1, head_dim=64, dtype=2, causal=1,
+                 scale=0.125):
+    return [None] + [ptr] * 16 + [batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal, scale]
+
+
+@pytest.mark.parametrize("kwargs,status,needle", [
+    (dict(ptr=None), 1, "q is null"),
+    (dict(ptr=8), 1, "not 16-byte aligned"),
+    (dict(batch=0), 1, "sizes must be >= 1"),
+    (dict(n_k=0), 1, "sizes must be >= 1"),
+    (dict(dtype=7), 1, "unknown dtype"),
+    (dict(heads=3, kv_heads=2), 1, "multiple of kv_heads"),
+    (dict(heads=4, kv_heads=2), 2, "grouped-query"),
+    (dict(head_dim=96), 2, "head_dim must be 64 or 128"),
+    (dict(head_dim=128, dtype=0), 2, "fp32 supports head_dim 64"),
+    (dict(scale=float("nan")), 1, "scale"),
+])
+def test_bwdbwd_rejects_invalid_arguments(lib, kwargs, status, needle):
+    st = lib.fhog_attention_bwdbwd(*_bwdbwd_args(**kwargs))
+    assert st == status
+    assert needle in lib.fhog_last_error().decode()
+
+
+def test_fwd_and_bwd_reject_invalid_arguments(lib):
+    st = lib.fhog_attention_fwd(None, None, 16, 16, 16, 16, 1, 8, 8, 1, 1, 64, 2, 0, 0.125)
+    assert st == 1 and "q is null" in lib.fhog_last_error().decode()
+    st = lib.fhog_attention_bwd(None, *([16] * 9), None, 1, 8, 8, 1, 1, 64, 2, 0, 0.125)
+    assert st == 1 and "delta is null" in lib.fhog_last_error().decode()
+
+
+def test_error_message_is_per_thread(lib):
+    import threading
+
+    lib.fhog_attention_bwdbwd(*_bwdbwd_args(ptr=None))
+    seen = {}
+
+    def other():
+        seen["msg"] = lib.fhog_last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == b""
+    assert b"q is null" in lib.fhog_last_error()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    from flash_hog import _hip
+
+    monkeypatch.setenv(_hip.LIB_ENV, str(tmp_path / "nope.so"))
+    _hip.lib.cache_clear()
+    try:
+        with pytest.raises(ImportError, match="not found"):
+            _hip.lib()
+    finally:
+        monkeypatch.delenv(_hip.LIB_ENV)
+        _hip.lib.cache_clear()

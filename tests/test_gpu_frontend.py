@@ -1,0 +1,80 @@
+"""Grad-of-grad through the public front-end, mirroring the reference's tests.
+
+tests/test_jax_fhog.py:56-62 builds vjp(f) with f(Q, K, V, dO) = vjp(attn)(dO)
+and compares it with XLA autodiff of jax.nn.dot_product_attention
+(make_reference_dpa_bwd_bwd, :26-34). Here the same composition runs through
+flash_hog.dot_product_attention (HIP forward, first backward and double
+backward) and is compared with the torch-CPU autodiff oracle in float64.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import TOL, default_scale, make_inputs, rel_err
+from oracle import autodiff
+
+pytestmark = pytest.mark.gpu
+
+
+def fhog_bwd_bwd(q, k, v, do, ddq, ddk, ddv, is_causal, scale):
+    import flash_hog
+
+    q, k, v, do = (t.detach().requires_grad_(True) for t in (q, k, v, do))
+    out = flash_hog.dot_product_attention(q, k, v, is_causal=is_causal, scale=scale)
+    dq, dk, dv = torch.autograd.grad(out, (q, k, v), do, create_graph=True)
+    return torch.autograd.grad((dq, dk, dv), (q, k, v, do), (ddq, ddk, ddv)), (out, dq, dk, dv)
+
+
+@pytest.mark.parametrize("is_causal", [True, False], ids=["causal", "noncausal"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_backward_backward_single(is_causal, dtype, cuda_device):
+    print("[case] frontend grad-of-grad", dtype, is_causal, flush=True)
+    x = make_inputs(2, 192, 192, 4, 64, dtype, seed=42)
+    scale = default_scale(64)
+    dev = {n: t.to(cuda_device) for n, t in x.items()}
+    (dq2, dk2, dv2, ddo), (out, dq, dk, dv) = fhog_bwd_bwd(
+        dev["q"], dev["k"], dev["v"], dev["do"], dev["ddq"], dev["ddk"], dev["ddv"], is_causal, scale)
+    torch.cuda.synchronize()
+    c = {n: t.double() for n, t in x.items()}
+    ref2 = autodiff.double_vjp(c["q"], c["k"], c["v"], c["do"], c["ddq"], c["ddk"], c["ddv"], scale, is_causal)
+    ref1 = autodiff.first_vjp(c["q"], c["k"], c["v"], c["do"], scale, is_causal)
+    ref_out = autodiff.attention(c["q"], c["k"], c["v"], scale, is_causal)
+    assert rel_err(out, ref_out) < TOL[dtype]
+    for a, r, n in zip((dq, dk, dv), ref1, ("dq", "dk", "dv")):
+        assert rel_err(a, r) < TOL[dtype], n
+    for a, r, n in zip((dq2, dk2, dv2, ddo), ref2, ("dq2", "dk2", "dv2", "ddo")):
+        assert rel_err(a, r) < TOL[dtype], n
+
+
+def test_unbatched_inputs(cuda_device):
+    """(T, N, H) inputs get a batch axis added and removed (attention.py:39-47)."""
+    import flash_hog
+
+    print("[case] frontend unbatched", flush=True)
+    x = make_inputs(1, 64, 64, 2, 64, torch.bfloat16, seed=3)
+    q, k, v = (x[n][0].to(cuda_device) for n in ("q", "k", "v"))
+    out = flash_hog.dot_product_attention(q, k, v, is_causal=True)
+    out_b = flash_hog.dot_product_attention(q[None], k[None], v[None], is_causal=True)
+    assert out.shape == q.shape
+    assert torch.equal(out, out_b[0])
+
+
+def test_hvp_matches_double_vjp(cuda_device):
+    """A Hessian-vector product of a scalar loss runs the double backward."""
+    import flash_hog
+
+    print("[case] frontend hvp", flush=True)
+    x = make_inputs(1, 128, 128, 2, 64, torch.float32, seed=9)
+    q, k, v = (x[n].to(cuda_device).requires_grad_(True) for n in ("q", "k", "v"))
+    w = x["do"].to(cuda_device)
+    u = (x["ddq"].to(cuda_device), x["ddk"].to(cuda_device), x["ddv"].to(cuda_device))
+    loss = (flash_hog.dot_product_attention(q, k, v, is_causal=True) * w).sum()
+    g = torch.autograd.grad(loss, (q, k, v), create_graph=True)
+    hvp = torch.autograd.grad(g, (q, k, v), u)
+    torch.cuda.synchronize()
+    c = {n: t.double() for n, t in x.items()}
+    ref = autodiff.double_vjp(c["q"], c["k"], c["v"], c["do"], c["ddq"], c["ddk"], c["ddv"], 0.125, True)
+    for a, r in zip(hvp, ref[:3]):
+        assert rel_err(a, r) < 1e-3

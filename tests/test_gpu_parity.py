@@ -1,0 +1,149 @@
+"""GPU parity of the HIP kernels against the CPU oracle (fp64) and the golden vectors.
+
+Every kernel is called through the C ABI (flash_hog/_hip.py). Inputs are the
+same seeded tensors for both sides; the oracle runs in float64 on the values
+after rounding to the kernel's dtype. Tolerances (tests/helpers.py TOL):
+max|a - r| / max|r| below 1e-3 for fp32, below 2e-2 for bf16 and fp16.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import DEGENERATE_FLOOR, TOL, default_scale, make_inputs, rel_err, to_np
+from oracle import attention as ora
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16 = torch.float32, torch.float16, torch.bfloat16
+
+# (id, batch, n_q, n_k, heads, head_dim, dtype, causal, qkv_scale)
+CASES = [
+    ("plumbing_f32_causal", 1, 256, 256, 2, 64, F32, True, 1.0),
+    ("bf16_causal", 2, 256, 256, 3, 64, BF16, True, 1.0),
+    ("bf16_noncausal", 2, 256, 256, 3, 64, BF16, False, 1.0),
+    ("f16_ragged_noncausal", 1, 1000, 1000, 2, 64, F16, False, 0.5),
+    ("bf16_ragged_causal", 1, 200, 200, 2, 64, BF16, True, 1.0),
+    ("bf16_d128_causal", 1, 320, 320, 2, 128, BF16, True, 1.0),
+    ("f16_d128_ragged_rect", 1, 100, 70, 1, 128, F16, False, 1.0),
+    ("bf16_rect_noncausal", 1, 128, 256, 2, 64, BF16, False, 1.0),
+    ("bf16_rect_causal", 1, 192, 256, 2, 64, BF16, True, 1.0),
+    ("f32_noncausal_ragged", 2, 77, 45, 2, 64, F32, False, 1.0),
+    ("f32_single_token", 1, 1, 1, 1, 64, F32, True, 1.0),
+]
+IDS = [c[0] for c in CASES]
+
+
+def _announce(*what):
+    print("[case]", *what, flush=True)
+
+
+def _oracle_residual(x, scale, causal, dtype):
+    """O (rounded to dtype) and L (fp32) from the fp64 oracle forward."""
+    o, lse = ora.attn_fwd(to_np(x["q"]), to_np(x["k"]), to_np(x["v"]), scale, causal)
+    return torch.from_numpy(o).to(dtype), torch.from_numpy(lse).float()
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_fwd_matches_oracle(case, cuda_device):
+    name, B, Nq, Nk, H, D, dtype, causal, qs = case
+    _announce("fwd", name)
+    x = make_inputs(B, Nq, Nk, H, D, dtype, seed=11, qkv_scale=qs)
+    scale = default_scale(D)
+    from flash_hog import _hip
+
+    o, lse = _hip.attention_fwd(x["q"].to(cuda_device), x["k"].to(cuda_device), x["v"].to(cuda_device),
+                                causal, scale)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = ora.attn_fwd(to_np(x["q"]), to_np(x["k"]), to_np(x["v"]), scale, causal)
+    assert rel_err(o, o_ref) < TOL[dtype]
+    assert np.max(np.abs(to_np(lse) - lse_ref)) < 1e-3 * max(1.0, np.max(np.abs(lse_ref)))
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_bwd_matches_oracle(case, cuda_device):
+    name, B, Nq, Nk, H, D, dtype, causal, qs = case
+    _announce("bwd", name)
+    x = make_inputs(B, Nq, Nk, H, D, dtype, seed=23, qkv_scale=qs)
+    scale = default_scale(D)
+    o, lse = _oracle_residual(x, scale, causal, dtype)
+    from flash_hog import _hip
+
+    g = lambda t: t.to(cuda_device)
+    dq, dk, dv, delta = _hip.attention_bwd(g(x["q"]), g(x["k"]), g(x["v"]), g(o), g(x["do"]), g(lse),
+                                           causal, scale)
+    torch.cuda.synchronize()
+    ref = ora.attn_bwd(to_np(x["q"]), to_np(x["k"]), to_np(x["v"]), to_np(o), to_np(x["do"]),
+                       to_np(lse), scale, causal)
+    for got, want, label in zip((dq, dk, dv, delta), ref, ("dq", "dk", "dv", "D")):
+        err = rel_err(got, want, DEGENERATE_FLOOR)
+        assert err < TOL[dtype], f"{label}: rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=IDS)
+def test_bwdbwd_matches_oracle(case, cuda_device):
+    name, B, Nq, Nk, H, D, dtype, causal, qs = case
+    _announce("bwdbwd", name)
+    x = make_inputs(B, Nq, Nk, H, D, dtype, seed=37, qkv_scale=qs)
+    scale = default_scale(D)
+    o, lse = _oracle_residual(x, scale, causal, dtype)
+    from flash_hog import _hip
+
+    g = lambda t: t.to(cuda_device)
+    dq2, dk2, dv2, ddo, stats = _hip.attention_bwdbwd(
+        g(x["q"]), g(x["k"]), g(x["v"]), g(o), g(x["do"]), g(x["ddq"]), g(x["ddk"]), g(x["ddv"]), g(lse),
+        causal, scale, return_stats=True)
+    torch.cuda.synchronize()
+    ref = ora.attn_bwd_bwd_stats(*(to_np(x[n]) for n in ("q", "k", "v")), to_np(o), to_np(x["do"]),
+                                 *(to_np(x[n]) for n in ("ddq", "ddk", "ddv")), to_np(lse), scale, causal,
+                                 return_stats=True)
+    got = (dq2, dk2, dv2, ddo) + tuple(stats)
+    for a, r, label in zip(got, ref, ("dq2", "dk2", "dv2", "ddo", "D", "dD", "B")):
+        err = rel_err(a, r, DEGENERATE_FLOOR)
+        assert err < TOL[dtype], f"{label}: rel err {err:.3e}"
+        assert torch.isfinite(torch.as_tensor(a)).all(), label
+
+
+def _golden():
+    import pathlib
+
+    path = pathlib.Path(__file__).resolve().parent / "golden" / "test_data.npz"
+    return dict(np.load(path))
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_bwdbwd_golden_vectors(dtype, cuda_device):
+    """The reference's test_data.zip (non-causal, 128 x 256 x 64, scale 1/8)
+    through the HIP double backward, with the fixture's own O and L."""
+    _announce("golden", dtype)
+    z = _golden()
+    t = lambda n: torch.from_numpy(z[n])[None, :, None, :].to(dtype).to(cuda_device)
+    lse = torch.from_numpy(z["L"])[None, None, :].float().to(cuda_device)
+    from flash_hog import _hip
+
+    outs = _hip.attention_bwdbwd(t("q"), t("k"), t("v"), t("o"), t("do"), t("ddq"), t("ddk"), t("ddv"), lse,
+                                 False, 0.125)
+    torch.cuda.synchronize()
+    for a, n in zip(outs, ("dq2", "dk2", "dv2", "ddo")):
+        err = rel_err(a[0, :, 0, :], z[n])
+        # the fixture itself carries bf16-level error (its L is a bf16-precision logsumexp)
+        assert err < 2e-2, f"{n}: rel err {err:.3e}"
+
+
+def test_gpu_reference_matches_oracle(cuda_device):
+    """Pins the fp32 GPU checker used at full size against the fp64 oracle."""
+    import gpu_reference
+
+    _announce("gpu_reference pin")
+    x = make_inputs(1, 160, 160, 2, 64, F32, seed=5)
+    scale = default_scale(64)
+    o, lse = _oracle_residual(x, scale, True, F32)
+    g = lambda t: t.to(cuda_device)
+    got = gpu_reference.bwdbwd(*(g(x[n]) for n in ("q", "k", "v")), g(o), g(x["do"]),
+                               *(g(x[n]) for n in ("ddq", "ddk", "ddv")), g(lse), scale, True)
+    ref = ora.attn_bwd_bwd_stats(*(to_np(x[n]) for n in ("q", "k", "v")), to_np(o), to_np(x["do"]),
+                                 *(to_np(x[n]) for n in ("ddq", "ddk", "ddv")), to_np(lse), scale, True)
+    for a, r in zip(got, ref):
+        assert rel_err(a, r) < 1e-4
