@@ -1,0 +1,259 @@
+"""Benchmark: attention double backward (Flash-HOG) on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Workload: B=4, N=2048, H=16, D=64, bf16, causal, scale 1/sqrt(64); seeded
+N(0, 1) inputs resident in HBM. One step = one fhog_attention_bwdbwd call
+(D precompute, passes 1-3, pass 4) given (q, k, v, O, L, dO, ddQ, ddK, ddV),
+O and L coming from this library's own forward.
+
+value = algorithmic TFLOP/s of the whole double backward: 24 * d flops per
+unmasked (query, key) pair (the 12 distinct N_Q x N_K x d products; the
+recomputation the passes do is not counted), divided by the measured time.
+The roofline block describes the dominant kernel, stage 1 (passes 1-3), whose
+algorithmic share is the 9 products it is first to need (18 * d per pair),
+timed per launch with HIP events on the stream it runs on.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import pathlib
+import sys
+import time
+
+REPO = pathlib.Path(__file__).resolve().parent
+for _p in (REPO, REPO / "flash-hog_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+MI355X_PEAK_BF16_TFLOPS = 2516.6  # dense bf16 MFMA
+MI355X_PEAK_HBM_GBS = 8000.0
+
+WORKLOAD = dict(batch=4, seq=2048, heads=16, head_dim=64, dtype="bf16", causal=True)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def unmasked_pairs(n_q, n_k, causal):
+    if not causal:
+        return n_q * n_k
+    full = min(n_q, n_k)
+    return full * (full + 1) // 2 + max(0, n_q - n_k) * n_k
+
+
+def make_inputs(torch, B, N, H, D, dtype, device, seed=0):
+    names = ("q", "k", "v", "do", "ddq", "ddk", "ddv")
+    out = {}
+    for i, n in enumerate(names):
+        gen = torch.Generator().manual_seed(seed + i)
+        out[n] = torch.randn((B, N, H, D), generator=gen).to(dtype).to(device)
+    return out
+
+
+def cpu_baseline(args, B, N, H, D, scale, causal):
+    """The reference's CPU path restated: torch-CPU fp32 autograd double VJP of
+    materialised attention (oracle/autodiff.py), one (batch, head) slice at a
+    time, over the whole workload or until about args.cpu_seconds elapse."""
+    import torch
+
+    from oracle import autodiff
+
+    cores = min(len(os.sched_getaffinity(0)), args.cpu_threads)
+    torch.set_num_threads(cores)
+    names = ("q", "k", "v", "do", "ddq", "ddk", "ddv")
+
+    def slice_inputs(i):
+        gen = torch.Generator().manual_seed(1000 + i)
+        return [torch.randn((1, N, 1, D), generator=gen) for _ in names]
+
+    autodiff.double_vjp(*slice_inputs(0), scale, causal)  # warm-up
+    done, busy = 0, 0.0
+    while done < B * H and busy < args.cpu_seconds:
+        xs = slice_inputs(done)
+        t0 = time.perf_counter()
+        autodiff.double_vjp(*xs, scale, causal)
+        busy += time.perf_counter() - t0
+        done += 1
+    flops = 24.0 * D * unmasked_pairs(N, N, causal) * done
+    return {
+        "value": flops / busy / 1e12,
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{done} of the {B * H} (batch, head) slices of B{B} N{N} H{H} D{D} causal, fp32 torch-CPU "
+                   f"autograd double VJP of materialised attention (oracle/autodiff.py), {busy:.1f} s"),
+        "ms_per_slice": busy / done * 1e3,
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description="Flash-HOG double-backward benchmark")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="run one device copy of this many MiB first (PMC byte-counter calibration)")
+    args = ap.parse_args(argv)
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the double backward shards over "
+              f"(batch, head) with no exchange, so whole-job throughput at N GPUs is N x the one-GPU value.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from flash_hog import _hip
+
+    dev = torch.device("cuda:0")
+    B, N, H, D = WORKLOAD["batch"], WORKLOAD["seq"], WORKLOAD["heads"], WORKLOAD["head_dim"]
+    causal = WORKLOAD["causal"]
+    dtype = torch.bfloat16
+    scale = 1.0 / math.sqrt(D)
+    lib = _hip.lib()
+
+    if args.calibrate_copy_mib:
+        n = args.calibrate_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, device=dev, dtype=torch.float32)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log(f"calibration copy: {args.calibrate_copy_mib} MiB read + written")
+
+    x = make_inputs(torch, B, N, H, D, dtype, dev)
+    o, lse = _hip.attention_fwd(x["q"], x["k"], x["v"], causal, scale)
+    dq2, dk2, dv2, ddo = (torch.empty_like(x[n]) for n in ("q", "k", "v", "do"))
+    stats = torch.empty((3, B, H, N), device=dev, dtype=torch.float32)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream(dev)
+    s_ptr = stream.cuda_stream
+    common = (x["q"].data_ptr(), x["k"].data_ptr(), x["v"].data_ptr(), o.data_ptr(), x["do"].data_ptr(),
+              x["ddq"].data_ptr(), x["ddk"].data_ptr(), x["ddv"].data_ptr(), lse.data_ptr(),
+              dq2.data_ptr(), dk2.data_ptr(), dv2.data_ptr(), ddo.data_ptr(),
+              stats[0].data_ptr(), stats[1].data_ptr(), stats[2].data_ptr())
+    dims = (B, N, N, H, H, D, _hip.DTYPE_CODES[dtype], int(causal), scale)
+
+    def step():
+        _hip.check(lib.fhog_attention_bwdbwd(s_ptr, *common, *dims))
+
+    def stage(k):
+        _hip.check(lib.fhog_attention_bwdbwd_stage(s_ptr, k, *common, *dims))
+
+    mem0 = torch.cuda.memory_allocated(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: exactly `steps` double backwards.
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = gpu_ms / args.steps
+    log(f"double backward: {ms_per_step:.4f} ms/step (events), wall {wall * 1e3 / args.steps:.4f} ms/step")
+
+    # Per-kernel timing of both stages with events on the launch stream.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for e in evs:
+        e[0].record(stream)
+        stage(1)
+        e[1].record(stream)
+        stage(2)
+        e[2].record(stream)
+    torch.cuda.synchronize()
+    s1_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    s2_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    log(f"stage 1 (passes 1-3): {s1_ms:.4f} ms, stage 2 (pass 4): {s2_ms:.4f} ms")
+
+    pairs = unmasked_pairs(N, N, causal) * B * H
+    alg_flops = 24.0 * D * pairs
+    value = alg_flops / (ms_per_step * 1e-3) / 1e12
+    s1_alg = 18.0 * D * pairs
+    s1_tflops = s1_alg / (s1_ms * 1e-3) / 1e12
+    # executed MFMA work: stage 1 = 14 products per streamed tile pair, stage 2 = 8
+    exec_tflops = (28.0 + 16.0) * D * pairs / (ms_per_step * 1e-3) / 1e12
+
+    # Peak memory of one call with torch-owned outputs, against the inputs.
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    _hip.attention_bwdbwd(x["q"], x["k"], x["v"], o, x["do"], x["ddq"], x["ddk"], x["ddv"], lse, causal, scale)
+    torch.cuda.synchronize()
+    peak_extra = torch.cuda.max_memory_allocated(dev) - base
+
+    # End-to-end HVP (forward + first backward + double backward), as the reference benchmarks.
+    torch.cuda.synchronize()
+    for _ in range(3):
+        o2, l2 = _hip.attention_fwd(x["q"], x["k"], x["v"], causal, scale)
+        _hip.attention_bwd(x["q"], x["k"], x["v"], o2, x["do"], l2, causal, scale)
+        _hip.attention_bwdbwd(x["q"], x["k"], x["v"], o2, x["do"], x["ddq"], x["ddk"], x["ddv"], l2, causal, scale)
+    torch.cuda.synchronize()
+    h0, h1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    h0.record(stream)
+    reps = 10
+    for _ in range(reps):
+        o2, l2 = _hip.attention_fwd(x["q"], x["k"], x["v"], causal, scale)
+        _hip.attention_bwd(x["q"], x["k"], x["v"], o2, x["do"], l2, causal, scale)
+        _hip.attention_bwdbwd(x["q"], x["k"], x["v"], o2, x["do"], x["ddq"], x["ddk"], x["ddv"], l2, causal, scale)
+    h1.record(stream)
+    torch.cuda.synchronize()
+    hvp_ms = h0.elapsed_time(h1) / reps
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(args, B, N, H, D, scale, causal)
+        log(f"cpu baseline: {cpu['value']:.4f} TFLOP/s on {cpu['cores']} cores ({cpu['sample']})")
+
+    result = {
+        "metric": "double-bwd TFLOP/s + % bf16 MFMA peak, B4 H16 N2048 D64 causal",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "attention double backward (Flash-HOG), causal", "batch": B, "seq_len": N,
+                   "heads": H, "head_dim": D, "scale": scale, "parallelism": "none (1 GPU)"},
+        "pct_of_bf16_peak": round(100.0 * value / MI355X_PEAK_BF16_TFLOPS, 3),
+        "roofline": {"bound": "mfma", "kernel": "bwdbwd_q_kernel (stage 1, passes 1-3)",
+                     "achieved": round(s1_tflops, 3), "peak": MI355X_PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(s1_tflops / MI355X_PEAK_BF16_TFLOPS, 5), "traffic": None,
+                     "alg_flops_per_launch": s1_alg, "ms_per_launch": round(s1_ms, 5)},
+        "cpu_baseline": None if cpu is None else {k: (round(v, 6) if isinstance(v, float) else v)
+                                                  for k, v in cpu.items()},
+        "detail": {"stage2_ms": round(s2_ms, 5), "executed_mfma_tflops": round(exec_tflops, 3),
+                   "alg_gflop_per_step": round(alg_flops / 1e9, 3), "peak_extra_hbm_bytes": int(peak_extra),
+                   "hvp_ms": round(hvp_ms, 5), "wall_ms_per_step": round(wall * 1e3 / args.steps, 5)},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

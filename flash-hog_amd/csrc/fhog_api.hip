@@ -151,28 +151,54 @@ int fhog_attention_bwd(fhog_stream_t stream, const void* q, const void* k, const
   return launch_status(dispatch(dtype, head_dim, causal != 0, run), who);
 }
 
-int fhog_attention_bwdbwd(fhog_stream_t stream, const void* q, const void* k, const void* v, const void* o,
-                          const void* dout, const void* ddq, const void* ddk, const void* ddv, const float* lse,
-                          void* dq2, void* dk2, void* dv2, void* ddo, float* delta, float* ddelta, float* bstat,
-                          int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim, int dtype, int causal,
-                          float scale) {
-  static const char* who = "fhog_attention_bwdbwd";
+namespace {
+
+int bwdbwd_impl(const char* who, int stages, fhog_stream_t stream, const void* q, const void* k, const void* v,
+                const void* o, const void* dout, const void* ddq, const void* ddk, const void* ddv,
+                const float* lse, void* dq2, void* dk2, void* dv2, void* ddo, float* delta, float* ddelta,
+                float* bstat, int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim, int dtype,
+                int causal, float scale) {
   const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, scale};
   if (int st = check_shape(s, who)) return st;
-  if (int st = check_ptrs(who, {{"q", q}, {"k", k}, {"v", v}, {"o", o}, {"dout", dout}, {"ddq", ddq},
-                                {"ddk", ddk}, {"ddv", ddv}, {"dq2", dq2}, {"dk2", dk2}, {"dv2", dv2},
-                                {"ddo", ddo}},
+  if (int st = check_ptrs(who, {{"q", q}, {"k", k}, {"v", v}, {"dout", dout}, {"ddq", ddq}, {"ddk", ddk},
+                                {"ddv", ddv}},
                            {{"lse", lse}, {"delta", delta}, {"ddelta", ddelta}, {"bstat", bstat}}))
     return st;
+  if (stages & 1)
+    if (int st = check_ptrs(who, {{"o", o}, {"dq2", dq2}, {"ddo", ddo}}, {})) return st;
+  if (stages & 2)
+    if (int st = check_ptrs(who, {{"dk2", dk2}, {"dv2", dv2}}, {})) return st;
   auto run = [&]<typename T, int D, bool C>() {
     fhog::BwdBwdParams<T> p{(const T*)q,   (const T*)k,   (const T*)v,   (const T*)o, (const T*)dout,
                             (const T*)ddq, (const T*)ddk, (const T*)ddv, lse,         (T*)dq2,
                             (T*)dk2,       (T*)dv2,       (T*)ddo,       delta,       ddelta,
                             bstat,         batch,         n_q,           n_k,         heads,
                             scale};
-    return fhog::launch_bwdbwd<T, D, C>(p, (hipStream_t)stream);
+    return fhog::launch_bwdbwd<T, D, C>(p, (hipStream_t)stream, stages);
   };
   return launch_status(dispatch(dtype, head_dim, causal != 0, run), who);
+}
+
+}  // namespace
+
+int fhog_attention_bwdbwd(fhog_stream_t stream, const void* q, const void* k, const void* v, const void* o,
+                          const void* dout, const void* ddq, const void* ddk, const void* ddv, const float* lse,
+                          void* dq2, void* dk2, void* dv2, void* ddo, float* delta, float* ddelta, float* bstat,
+                          int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim, int dtype, int causal,
+                          float scale) {
+  return bwdbwd_impl("fhog_attention_bwdbwd", 3, stream, q, k, v, o, dout, ddq, ddk, ddv, lse, dq2, dk2, dv2,
+                     ddo, delta, ddelta, bstat, batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal, scale);
+}
+
+int fhog_attention_bwdbwd_stage(fhog_stream_t stream, int stage, const void* q, const void* k, const void* v,
+                                const void* o, const void* dout, const void* ddq, const void* ddk,
+                                const void* ddv, const float* lse, void* dq2, void* dk2, void* dv2, void* ddo,
+                                float* delta, float* ddelta, float* bstat, int batch, int n_q, int n_k,
+                                int heads, int kv_heads, int head_dim, int dtype, int causal, float scale) {
+  static const char* who = "fhog_attention_bwdbwd_stage";
+  if (stage != 1 && stage != 2) return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: stage must be 1 or 2, got %d", who, stage);
+  return bwdbwd_impl(who, stage, stream, q, k, v, o, dout, ddq, ddk, ddv, lse, dq2, dk2, dv2, ddo, delta,
+                     ddelta, bstat, batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal, scale);
 }
 
 }  // extern "C"

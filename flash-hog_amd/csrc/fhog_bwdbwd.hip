@@ -420,18 +420,23 @@ __global__ void __launch_bounds__(kThreads) bwdbwd_k_kernel(BwdBwdParams<T> p) {
 }  // namespace
 
 template <typename T, int D, bool CAUSAL>
-hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream) {
+hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stages) {
   const int nbh = p.batch * p.heads;
   const int nqb = (p.nq + 32 * kWaves - 1) / (32 * kWaves);
   const int nkb = (p.nk + 32 * kWaves - 1) / (32 * kWaves);
-  hipLaunchKernelGGL((bwdbwd_q_kernel<T, D, CAUSAL>), dim3(nqb * nbh), dim3(kThreads), 0, stream, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL>), dim3(nkb * nbh), dim3(kThreads), 0, stream, p);
-  return hipGetLastError();
+  if (stages & 1) {
+    hipLaunchKernelGGL((bwdbwd_q_kernel<T, D, CAUSAL>), dim3(nqb * nbh), dim3(kThreads), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (stages & 2) {
+    hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL>), dim3(nkb * nbh), dim3(kThreads), 0, stream, p);
+    return hipGetLastError();
+  }
+  return hipSuccess;
 }
 
-#define FHOG_INST(T, D, C) template hipError_t launch_bwdbwd<T, D, C>(const BwdBwdParams<T>&, hipStream_t);
+#define FHOG_INST(T, D, C) template hipError_t launch_bwdbwd<T, D, C>(const BwdBwdParams<T>&, hipStream_t, int);
 FHOG_INST(__bf16, 64, true)
 FHOG_INST(__bf16, 64, false)
 FHOG_INST(__bf16, 128, true)

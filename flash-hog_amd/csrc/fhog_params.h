@@ -38,6 +38,8 @@ template <typename T> struct BwdBwdParams {
 
 template <typename T, int D, bool CAUSAL> hipError_t launch_fwd(const FwdParams<T>& p, hipStream_t s);
 template <typename T, int D, bool CAUSAL> hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t s);
-template <typename T, int D, bool CAUSAL> hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t s);
+// stages: bit 0 = stage 1 (passes 1-3), bit 1 = stage 2 (pass 4).
+template <typename T, int D, bool CAUSAL>
+hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t s, int stages = 3);
 
 }  // namespace fhog

@@ -41,6 +41,7 @@ SIGNATURES = {
     "fhog_attention_fwd": (_i, [_p, _p, _p, _p, _p, _p] + [_i] * 8 + [_f]),
     "fhog_attention_bwd": (_i, [_p] * 11 + [_i] * 8 + [_f]),
     "fhog_attention_bwdbwd": (_i, [_p] * 17 + [_i] * 8 + [_f]),
+    "fhog_attention_bwdbwd_stage": (_i, [_p, _i] + [_p] * 16 + [_i] * 8 + [_f]),
 }
 
 

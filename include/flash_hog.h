@@ -108,6 +108,27 @@ int fhog_attention_bwdbwd(fhog_stream_t stream,
                           int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim,
                           int dtype, int causal, float scale);
 
+/*
+ * One stage of fhog_attention_bwdbwd: stage 1 = passes 1-3 (tiled over
+ * queries; computes D, dD, B into delta/ddelta/bstat and writes dq2, ddo),
+ * stage 2 = pass 4 (tiled over keys; reads delta/ddelta/bstat, writes dk2,
+ * dv2). Running stage 1 then stage 2 on one stream equals
+ * fhog_attention_bwdbwd. The reference's handler always launches both
+ * (ffi.cu:71-73); the split exists so that the stages can be timed, profiled
+ * or ordered by the caller (stage 2 must see stage 1's statistics). Pointers
+ * a stage does not touch may be null: stage 1 ignores dk2, dv2; stage 2
+ * ignores o, dq2, ddo.
+ */
+int fhog_attention_bwdbwd_stage(fhog_stream_t stream, int stage,
+                                const void* q, const void* k, const void* v,
+                                const void* o, const void* dout,
+                                const void* ddq, const void* ddk, const void* ddv,
+                                const float* lse,
+                                void* dq2, void* dk2, void* dv2, void* ddo,
+                                float* delta, float* ddelta, float* bstat,
+                                int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim,
+                                int dtype, int causal, float scale);
+
 #ifdef __cplusplus
 }
 #endif
