@@ -34,19 +34,35 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 
+// Waves per SIMD the register allocator is asked to allow: two for 2-byte
+// types at D = 64 (so one wave's matrix work overlaps the other's vector work),
+// one otherwise.
+template <typename T, int D> struct Occupancy {
+  static constexpr int value = (sizeof(T) == 2 && D == 64) ? 2 : 1;
+};
+
 // ----------------------------------------------------------------------------
 // Stage 1: passes 1-3, tiled over queries.
+//
+// Sweep 1 (passes 1+2) computes S, ddS, dP and, per row, dD = sum ddS P,
+// r2 = sum dP P, r3 = sum dP ddS P, and accumulates u = P ddV into the ddO
+// accumulator; then r1 = sum_j P dPa = <dO_i, u_i> and
+// B = r1 - dD r2 - D dD + r3. Sweep 2 (pass 3) recomputes S, ddS, dP, dPa and
+// adds dS ddK + dS2 K to dQ2 and ddP V to ddO (whose P ddV part came from
+// sweep 1). Key-side tiles go global -> LDS directly (no registers) into a
+// two-stage ring with one barrier per tile.
 // ----------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL>
-__global__ void __launch_bounds__(kThreads) bwdbwd_q_kernel(BwdBwdParams<T> p) {
-  typedef TileGeom<T, D> G;
+__global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
+bwdbwd_q_kernel(BwdBwdParams<T> p) {
+  typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;       // 16-deep steps over the head dim
   constexpr int DT = D / 32;       // 32-wide output column blocks
   constexpr int BQ = 32 * kWaves;  // queries per workgroup
   constexpr int BK = 32;           // keys per streamed tile
-  // tensors: 0 = K, 1 = V, 2 = ddK, 3 = ddV
-  __shared__ __attribute__((aligned(32))) T s_row[2][4][G::kRowElems];
-  __shared__ __attribute__((aligned(32))) T s_tr[2][4][G::kTrElems];
+  // [stage][tensor]: 0 = K, 1 = V, 2 = ddK, 3 = ddV
+  __shared__ __attribute__((aligned(1024))) T s_kv[2][4][G::kElems];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = lane & 31, g = lane >> 5;
@@ -82,127 +98,156 @@ __global__ void __launch_bounds__(kThreads) bwdbwd_q_kernel(BwdBwdParams<T> p) {
       dof[ks] = zero8<T>();
     }
   }
+  const float scale = p.scale;
+  const float c2 = scale * kLog2e;
   const float Di = xgroup_sum(dpart);
-  const float Li2 = qvalid ? p.lse[sbase + qi] * kLog2e : 0.f;
+  const float nL2 = qvalid ? -p.lse[sbase + qi] * kLog2e : 0.f;
+  const float nsD = -scale * Di;
 
   int kend = p.nk;
   if (CAUSAL) kend = min(kend, qb * BQ + BQ);
-  const int nkt = (kend + BK - 1) / BK;           // tiles the workgroup streams
+  const int nkt = (kend + BK - 1) / BK;                   // tiles the workgroup streams
   int wend = p.nk;
   if (CAUSAL) wend = min(wend, q0 + 32);
   const int wkt = q0 < p.nq ? (wend + BK - 1) / BK : 0;  // tiles with work for this wave
 
-  const float scale = p.scale;
-  const float c2 = scale * kLog2e;
-  float dd_acc = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
-  float ddi = 0.f, bi = 0.f;
-  f32x16 acc_dq2[DT], acc_ddo[DT];
+  const T* src = (wave == 0 ? p.k : wave == 1 ? p.v : wave == 2 ? p.ddk : p.ddv) + kbase;
+  const int total = 2 * nkt;
+  tile_load_lds<T, D>(s_kv[0][wave], src, rs, p.nk, lane);
+
+  // Waits for tile `it`, then starts streaming tile it + 1 (the key sequence is
+  // streamed twice) into the other stage.
+  auto advance = [&](int it) {
+    wait_vmem();
+    __syncthreads();
+    if (it + 1 < total) {
+      const int kn = it + 1 < nkt ? it + 1 : it + 1 - nkt;
+      tile_load_lds<T, D>(s_kv[(it + 1) & 1][wave], src + (long)kn * BK * rs, rs, p.nk - kn * BK, lane);
+    }
+  };
+  // P of the tile at stage `buf` (key tile kt), masked on diagonal / ragged tiles.
+  auto probs = [&](const f32x16& S, int kt) {
+    const int k0 = kt * BK;
+    const bool need_mask = (k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0);
+    const int klim = min(p.nk - 1, CAUSAL ? qi : p.nk - 1) - k0;  // last visible key, tile-relative
+    f32x16 P;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    acc_dq2[dt] = zero16();
-    acc_ddo[dt] = zero16();
+    for (int r = 0; r < 16; ++r) {
+      const float pv = exp2_fast(fmaf(S[r], c2, nL2));
+      P[r] = (need_mask && crow(r, g) > klim) ? 0.f : pv;
+    }
+    return P;
+  };
+
+  // ---- sweep 1: dD, r2, r3 and u = P ddV (into acc_ddo) ----
+  f32x16 acc_ddo[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc_ddo[dt] = zero16();
+  float dd_acc = 0.f, r2 = 0.f, r3 = 0.f;
+  for (int it = 0; it < nkt; ++it) {
+    advance(it);
+    if (it < wkt) {
+      const T* sK = s_kv[it & 1][0];
+      const T* sV = s_kv[it & 1][1];
+      const T* sdK = s_kv[it & 1][2];
+      const T* sdV = s_kv[it & 1][3];
+      f32x16 S = zero16(), ddS = zero16(), dP = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const V8<T> kf = frag_row_swz<T, D>(sK, n, g, ks);
+        S = mma<T>(kf, qf[ks], S);
+        ddS = mma<T>(kf, ddqf[ks], ddS);
+        ddS = mma<T>(frag_row_swz<T, D>(sdK, n, g, ks), qf[ks], ddS);
+        dP = mma<T>(frag_row_swz<T, D>(sV, n, g, ks), dof[ks], dP);
+      }
+      const f32x16 P = probs(S, it);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        dd_acc = fmaf(ddS[r], P[r], dd_acc);
+        r2 = fmaf(dP[r], P[r], r2);
+        r3 = fmaf(dP[r] * ddS[r], P[r], r3);
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const V8<T> oP = cvt8<T>(s ? hi8(P) : lo8(P));
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          acc_ddo[dt] = mma<T>(frag_tr_swz<T, D>(sdV, 32 * dt, lane, s), oP, acc_ddo[dt]);
+      }
+    }
   }
 
-  const T* src = wave == 0 ? p.k : wave == 1 ? p.v : wave == 2 ? p.ddk : p.ddv;
-  src += kbase;
-  TileRegs<T, D> pre;
-  tile_load<T, D>(pre, src, rs, p.nk, lane);
-  tile_store_lds<T, D>(pre, s_row[0][wave], s_tr[0][wave], lane);
-  __syncthreads();
-
-  for (int it = 0; it < 2 * nkt; ++it) {
-    const int kt = it < nkt ? it : it - nkt;
-    const int buf = it & 1;
-    const bool has_next = it + 1 < 2 * nkt;
-    if (has_next) {
-      const int ktn = it + 1 < nkt ? it + 1 : it + 1 - nkt;
-      tile_load<T, D>(pre, src + (long)ktn * BK * rs, rs, p.nk - ktn * BK, lane);
+  // r1 = <dO_i, u_i>: u is in the accumulator layout (lane = query, registers = columns).
+  float r1 = 0.f;
+  if (qvalid) {
+    const T* dorow = p.dout + qbase + (long)qi * rs;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const V4<T> x = *reinterpret_cast<const V4<T>*>(dorow + 32 * dt + 8 * a + 4 * g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r1 = fmaf((float)x[j], acc_ddo[dt][4 * a + j], r1);
+      }
     }
+  }
+  const float dD = xgroup_sum(dd_acc) * scale;
+  const float Bi = xgroup_sum(r1) - dD * xgroup_sum(r2) - Di * dD + xgroup_sum(r3) * scale;
+  if (qvalid && g == 0) {
+    p.delta[sbase + qi] = Di;
+    p.ddelta[sbase + qi] = dD;
+    p.bstat[sbase + qi] = Bi;
+  }
+  const float ndd = -dD, nsB = -scale * Bi;
+
+  // ---- sweep 2: dQ2 += dS ddK + dS2 K, ddO += ddP V ----
+  f32x16 acc_dq2[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc_dq2[dt] = zero16();
+  for (int it = nkt; it < total; ++it) {
+    advance(it);
+    const int kt = it - nkt;
     if (kt < wkt) {
-      const T* sK = s_row[buf][0];
-      const T* sV = s_row[buf][1];
-      const T* sdK = s_row[buf][2];
-      const T* sdV = s_row[buf][3];
+      const T* sK = s_kv[it & 1][0];
+      const T* sV = s_kv[it & 1][1];
+      const T* sdK = s_kv[it & 1][2];
+      const T* sdV = s_kv[it & 1][3];
       f32x16 S = zero16(), ddS = zero16(), dP = zero16(), dPa = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const V8<T> kf = frag_row<T, D>(sK, n, g, ks);
-        const V8<T> dkf = frag_row<T, D>(sdK, n, g, ks);
-        const V8<T> vf = frag_row<T, D>(sV, n, g, ks);
-        const V8<T> dvf = frag_row<T, D>(sdV, n, g, ks);
+        const V8<T> kf = frag_row_swz<T, D>(sK, n, g, ks);
         S = mma<T>(kf, qf[ks], S);
         ddS = mma<T>(kf, ddqf[ks], ddS);
-        ddS = mma<T>(dkf, qf[ks], ddS);
-        dP = mma<T>(vf, dof[ks], dP);
-        dPa = mma<T>(dvf, dof[ks], dPa);
+        ddS = mma<T>(frag_row_swz<T, D>(sdK, n, g, ks), qf[ks], ddS);
+        dP = mma<T>(frag_row_swz<T, D>(sV, n, g, ks), dof[ks], dP);
+        dPa = mma<T>(frag_row_swz<T, D>(sdV, n, g, ks), dof[ks], dPa);
       }
-      const int k0 = kt * BK;
-      const bool need_mask = (k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0);
-      f32x16 P;
+      const f32x16 P = probs(S, kt);
+      // one 16-key half at a time: compute, convert, multiply
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = exp2_fast(S[r] * c2 - Li2);
-        if (need_mask) {
-          const int kj = k0 + crow(r, g);
-          const bool ok = kj < p.nk && (!CAUSAL || kj <= qi);
-          pv = ok ? pv : 0.f;
+      for (int s = 0; s < 2; ++s) {
+        f32x8 vdS, vdS2, vddP;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int r = 8 * s + e;
+          const float t = fmaf(ddS[r], scale, ndd);            // ddS - dD
+          float w = fmaf(dP[r], t, dPa[r]);                     // dPa + dP (ddS - dD)
+          w = fmaf(ddS[r], nsD, w);                             //   - ddS D  = dP2
+          vdS[e] = P[r] * fmaf(dP[r], scale, nsD);              // scale P (dP - D)
+          vdS2[e] = P[r] * fmaf(w, scale, nsB);                 // scale P (dP2 - B)
+          vddP[e] = P[r] * t;                                   // P (ddS - dD)
         }
-        P[r] = pv;
-      }
-      if (it < nkt) {
-        // passes 1+2: per-lane partial row sums
+        const V8<T> oS = cvt8<T>(vdS);
+        const V8<T> oS2 = cvt8<T>(vdS2);
+        const V8<T> odP = cvt8<T>(vddP);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float pd = P[r] * dP[r];
-          dd_acc += ddS[r] * P[r];
-          r1 += dPa[r] * P[r];
-          r2 += pd;
-          r3 += pd * ddS[r];
-        }
-      } else {
-        // pass 3
-        f32x16 vdS, vdS2, vddP;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float ddss = ddS[r] * scale;
-          const float t = ddss - ddi;
-          const float dp = dP[r];
-          const float dp2 = dPa[r] + dp * t - ddss * Di;
-          const float ps = P[r] * scale;
-          vdS[r] = ps * (dp - Di);
-          vdS2[r] = ps * (dp2 - bi);
-          vddP[r] = P[r] * t;
-        }
-        const T* tK = s_tr[buf][0];
-        const T* tV = s_tr[buf][1];
-        const T* tdK = s_tr[buf][2];
-        const T* tdV = s_tr[buf][3];
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const V8<T> oS = cvt8<T>(s ? hi8(vdS) : lo8(vdS));
-          const V8<T> oS2 = cvt8<T>(s ? hi8(vdS2) : lo8(vdS2));
-          const V8<T> odP = cvt8<T>(s ? hi8(vddP) : lo8(vddP));
-          const V8<T> oP = cvt8<T>(s ? hi8(P) : lo8(P));
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const int col = 32 * dt + n;
-            acc_dq2[dt] = mma<T>(frag_tr<T, D>(tdK, col, g, s), oS, acc_dq2[dt]);
-            acc_dq2[dt] = mma<T>(frag_tr<T, D>(tK, col, g, s), oS2, acc_dq2[dt]);
-            acc_ddo[dt] = mma<T>(frag_tr<T, D>(tV, col, g, s), odP, acc_ddo[dt]);
-            acc_ddo[dt] = mma<T>(frag_tr<T, D>(tdV, col, g, s), oP, acc_ddo[dt]);
-          }
+        for (int dt = 0; dt < DT; ++dt) {
+          acc_dq2[dt] = mma<T>(frag_tr_swz<T, D>(sdK, 32 * dt, lane, s), oS, acc_dq2[dt]);
+          acc_dq2[dt] = mma<T>(frag_tr_swz<T, D>(sK, 32 * dt, lane, s), oS2, acc_dq2[dt]);
+          acc_ddo[dt] = mma<T>(frag_tr_swz<T, D>(sV, 32 * dt, lane, s), odP, acc_ddo[dt]);
         }
       }
     }
-    if (it == nkt - 1) {
-      ddi = xgroup_sum(dd_acc) * scale;
-      const float R1 = xgroup_sum(r1);
-      const float R2 = xgroup_sum(r2);
-      const float R3 = xgroup_sum(r3) * scale;
-      bi = R1 - ddi * R2 - Di * ddi + R3;
-    }
-    if (has_next) tile_store_lds<T, D>(pre, s_row[buf ^ 1][wave], s_tr[buf ^ 1][wave], lane);
-    __syncthreads();
   }
 
   if (qvalid) {
@@ -223,27 +268,25 @@ __global__ void __launch_bounds__(kThreads) bwdbwd_q_kernel(BwdBwdParams<T> p) {
         *reinterpret_cast<V4<T>*>(ddo + d) = cvt4<T>(y);
       }
     }
-    if (g == 0) {
-      p.delta[sbase + qi] = Di;
-      p.ddelta[sbase + qi] = ddi;
-      p.bstat[sbase + qi] = bi;
-    }
   }
 }
 
 // ----------------------------------------------------------------------------
-// Stage 2: pass 4, tiled over keys.
+// Stage 2: pass 4, tiled over keys. Query-side tiles (Q, dO, ddQ) go
+// global -> LDS directly; the four row statistics of each query tile are
+// staged through registers as -L log2(e), -scale D, -dD, -scale B.
 // ----------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL>
-__global__ void __launch_bounds__(kThreads) bwdbwd_k_kernel(BwdBwdParams<T> p) {
-  typedef TileGeom<T, D> G;
+__global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
+bwdbwd_k_kernel(BwdBwdParams<T> p) {
+  typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
   constexpr int BKB = 32 * kWaves;  // keys per workgroup
   constexpr int BQ = 32;            // queries per streamed tile
-  // tensors: 0 = Q, 1 = dO, 2 = ddQ; statistics: 0 = L log2(e), 1 = D, 2 = dD, 3 = B
-  __shared__ __attribute__((aligned(32))) T s_row[2][3][G::kRowElems];
-  __shared__ __attribute__((aligned(32))) T s_tr[2][3][G::kTrElems];
+  // [stage][tensor]: 0 = Q, 1 = dO, 2 = ddQ
+  __shared__ __attribute__((aligned(1024))) T s_q[2][3][G::kElems];
   __shared__ __attribute__((aligned(16))) float s_stat[2][4][BQ];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -292,54 +335,44 @@ __global__ void __launch_bounds__(kThreads) bwdbwd_k_kernel(BwdBwdParams<T> p) {
     const float scale = p.scale;
     const float c2 = scale * kLog2e;
 
-    const T* src = wave == 0 ? p.q : wave == 1 ? p.dout : p.ddq;
-    src += qbase;
-    TileRegs<T, D> pre;
-    float2 st_pre;
-    // statistics loader: wave 3, lane -> (statistic lane/16, queries 2(lane%16) + {0,1})
-    const int st_id = lane >> 4, st_q = 2 * (lane & 15);
-    const float* st_src = st_id == 0 ? p.lse : st_id == 1 ? p.delta : st_id == 2 ? p.ddelta : p.bstat;
-    st_src += sbase;
-    const float st_mul = st_id == 0 ? kLog2e : 1.f;
-
-    auto load_tile = [&](int qt) {
-      const int q0 = qt * BQ;
-      if (wave < 3) {
-        tile_load<T, D>(pre, src + (long)q0 * rs, rs, p.nq - q0, lane);
-      } else {
-        const int qa = q0 + st_q;
-        st_pre.x = qa < p.nq ? st_src[qa] * st_mul : 0.f;
-        st_pre.y = qa + 1 < p.nq ? st_src[qa + 1] * st_mul : 0.f;
-      }
-    };
-    auto store_tile = [&](int buf) {
-      if (wave < 3) {
-        tile_store_lds<T, D>(pre, s_row[buf][wave], s_tr[buf][wave], lane);
-      } else {
-        *reinterpret_cast<float2*>(&s_stat[buf][st_id][st_q]) = st_pre;
-      }
+    // Wave w streams query-side tensor w (w < 3); every wave stages statistic w.
+    const T* src = (wave == 0 ? p.q : wave == 1 ? p.dout : p.ddq) + qbase;
+    const float* st_src = (wave == 0 ? p.lse : wave == 1 ? p.delta : wave == 2 ? p.ddelta : p.bstat) + sbase;
+    const float st_mul = wave == 0 ? -kLog2e : wave == 1 ? -scale : wave == 2 ? -1.f : -scale;
+    auto load_stat = [&](int qt) {
+      const int q = qt * BQ + n;
+      return (g == 0 && q < p.nq) ? st_src[q] * st_mul : 0.f;
     };
 
-    load_tile(qt_begin);
-    store_tile(0);
-    __syncthreads();
+    if (wave < 3) tile_load_lds<T, D>(s_q[0][wave], src + (long)qt_begin * BQ * rs, rs, p.nq - qt_begin * BQ, lane);
+    {
+      const float v = load_stat(qt_begin);
+      if (g == 0) s_stat[0][wave][n] = v;
+    }
 
     for (int qt = qt_begin; qt < nqt; ++qt) {
       const int buf = (qt - qt_begin) & 1;
       const bool has_next = qt + 1 < nqt;
-      if (has_next) load_tile(qt + 1);
+      wait_vmem();
+      __syncthreads();
+      float st_next = 0.f;
+      if (has_next) {
+        st_next = load_stat(qt + 1);
+        if (wave < 3)
+          tile_load_lds<T, D>(s_q[buf ^ 1][wave], src + (long)(qt + 1) * BQ * rs, rs, p.nq - (qt + 1) * BQ, lane);
+      }
       const int q0 = qt * BQ;
       const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0);
       if (active) {
-        const T* sQ = s_row[buf][0];
-        const T* sdO = s_row[buf][1];
-        const T* sdQ = s_row[buf][2];
+        const T* sQ = s_q[buf][0];
+        const T* sdO = s_q[buf][1];
+        const T* sdQ = s_q[buf][2];
         f32x16 S = zero16(), ddS = zero16(), dP = zero16(), dPa = zero16();
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const V8<T> qa = frag_row<T, D>(sQ, n, g, ks);
-          const V8<T> dqa = frag_row<T, D>(sdQ, n, g, ks);
-          const V8<T> doa = frag_row<T, D>(sdO, n, g, ks);
+          const V8<T> qa = frag_row_swz<T, D>(sQ, n, g, ks);
+          const V8<T> dqa = frag_row_swz<T, D>(sdQ, n, g, ks);
+          const V8<T> doa = frag_row_swz<T, D>(sdO, n, g, ks);
           S = mma<T>(qa, kf[ks], S);
           ddS = mma<T>(dqa, kf[ks], ddS);
           ddS = mma<T>(qa, dkf[ks], ddS);
@@ -347,52 +380,44 @@ __global__ void __launch_bounds__(kThreads) bwdbwd_k_kernel(BwdBwdParams<T> p) {
           dPa = mma<T>(doa, dvf[ks], dPa);
         }
         const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31);
-        f32x16 vdS, vdS2, vddP;
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const int m0 = 8 * a + 4 * g;
-          const f32x4 l2 = *reinterpret_cast<const f32x4*>(&s_stat[buf][0][m0]);
-          const f32x4 dv = *reinterpret_cast<const f32x4*>(&s_stat[buf][1][m0]);
-          const f32x4 ddv = *reinterpret_cast<const f32x4*>(&s_stat[buf][2][m0]);
-          const f32x4 bv = *reinterpret_cast<const f32x4*>(&s_stat[buf][3][m0]);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int r = 4 * a + j;
-            float pv = exp2_fast(S[r] * c2 - l2[j]);
-            if (need_mask) {
-              const int qg = q0 + m0 + j;
-              const bool ok = qg < p.nq && (!CAUSAL || qg >= kj);
-              pv = ok ? pv : 0.f;
-            }
-            const float ddss = ddS[r] * scale;
-            const float t = ddss - ddv[j];
-            const float dp = dP[r];
-            const float dp2 = dPa[r] + dp * t - ddss * dv[j];
-            const float ps = pv * scale;
-            vdS[r] = ps * (dp - dv[j]);
-            vdS2[r] = ps * (dp2 - bv[j]);
-            vddP[r] = pv * t;
-          }
-        }
-        const T* tQ = s_tr[buf][0];
-        const T* tdO = s_tr[buf][1];
-        const T* tdQ = s_tr[buf][2];
+        // visible iff query >= qmin (causal) and query < nq
+        const int qlo = (CAUSAL ? kj : 0) - q0, qhi = p.nq - q0;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const V8<T> oS = cvt8<T>(s ? hi8(vdS) : lo8(vdS));
-          const V8<T> oS2 = cvt8<T>(s ? hi8(vdS2) : lo8(vdS2));
-          const V8<T> odP = cvt8<T>(s ? hi8(vddP) : lo8(vddP));
+          f32x8 vdS, vdS2, vddP;
+#pragma unroll
+          for (int ah = 0; ah < 2; ++ah) {
+            const int a = 2 * s + ah;
+            const int m0 = 8 * a + 4 * g;
+            const f32x4 nl2 = *reinterpret_cast<const f32x4*>(&s_stat[buf][0][m0]);
+            const f32x4 nsd = *reinterpret_cast<const f32x4*>(&s_stat[buf][1][m0]);
+            const f32x4 ndd = *reinterpret_cast<const f32x4*>(&s_stat[buf][2][m0]);
+            const f32x4 nsb = *reinterpret_cast<const f32x4*>(&s_stat[buf][3][m0]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r = 4 * a + j, e = 4 * ah + j;
+              float pv = exp2_fast(fmaf(S[r], c2, nl2[j]));
+              if (need_mask) pv = (m0 + j < qlo || m0 + j >= qhi) ? 0.f : pv;
+              const float t = fmaf(ddS[r], scale, ndd[j]);
+              float w = fmaf(dP[r], t, dPa[r]);
+              w = fmaf(ddS[r], nsd[j], w);
+              vdS[e] = pv * fmaf(dP[r], scale, nsd[j]);
+              vdS2[e] = pv * fmaf(w, scale, nsb[j]);
+              vddP[e] = pv * t;
+            }
+          }
+          const V8<T> oS = cvt8<T>(vdS);
+          const V8<T> oS2 = cvt8<T>(vdS2);
+          const V8<T> odP = cvt8<T>(vddP);
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
-            const int col = 32 * dt + n;
-            acc_dk2[dt] = mma<T>(frag_tr<T, D>(tdQ, col, g, s), oS, acc_dk2[dt]);
-            acc_dk2[dt] = mma<T>(frag_tr<T, D>(tQ, col, g, s), oS2, acc_dk2[dt]);
-            acc_dv2[dt] = mma<T>(frag_tr<T, D>(tdO, col, g, s), odP, acc_dv2[dt]);
+            acc_dk2[dt] = mma<T>(frag_tr_swz<T, D>(sdQ, 32 * dt, lane, s), oS, acc_dk2[dt]);
+            acc_dk2[dt] = mma<T>(frag_tr_swz<T, D>(sQ, 32 * dt, lane, s), oS2, acc_dk2[dt]);
+            acc_dv2[dt] = mma<T>(frag_tr_swz<T, D>(sdO, 32 * dt, lane, s), odP, acc_dv2[dt]);
           }
         }
       }
-      if (has_next) store_tile(buf ^ 1);
-      __syncthreads();
+      if (has_next && g == 0) s_stat[buf ^ 1][wave][n] = st_next;
     }
   }
 

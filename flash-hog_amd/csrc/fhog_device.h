@@ -182,6 +182,125 @@ __device__ __forceinline__ V8<T> frag_tr(const T* __restrict__ transposed, int c
 __device__ __forceinline__ int crow(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 
 // ---------------------------------------------------------------------------
+// Swizzled tiles written straight from global memory into LDS.
+//
+// A tile is 32 rows x D columns, stored row-major without padding; each row is
+// split into 16-byte chunks and chunk c of row r is stored at chunk position
+// c ^ swz(r) (within aligned groups of 8 chunks). swz is a permutation of 0..7
+// over any 8 consecutive rows, so the 16-byte row reads of 8 consecutive rows
+// hit 8 different bank groups; and it maps any 4 consecutive rows starting at
+// a multiple of 4 to {0,2,4,6} or {1,3,5,7}, so the 2-chunk column slices the
+// transposed reads take from 4 consecutive rows are disjoint as well.
+//
+// global_load_lds with 16 bytes per lane writes lane l's data to
+// lds_base + 16 l, so lane l of load t fills chunk position l % CH of row
+// t * (64 / CH) + l / CH and fetches the logical chunk stored there.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+__device__ __forceinline__ int phys_chunk(int r, int c) { return (c & ~7) | ((c & 7) ^ swz(r)); }
+
+template <typename T, int D> struct SwzTile {
+  static constexpr int kRows = 32;
+  static constexpr int kRowBytes = D * (int)sizeof(T);
+  static constexpr int kChunks = kRowBytes / 16;        // 16-byte chunks per row
+  static constexpr int kRowsPerLoad = 64 / kChunks;     // rows one wave-wide 16-byte load fills
+  static constexpr int kLoads = kRows / kRowsPerLoad;   // wave-wide loads per tile
+  static constexpr int kElems = kRows * D;
+  static_assert(kChunks % 8 == 0 && kChunks <= 64, "row must be a multiple of 128 bytes");
+};
+
+// One wave-wide 16-byte-per-lane global -> LDS load: lane l's 16 bytes at
+// gptr land at lds_byte_addr + 16 l. Issued as inline assembly so that the
+// compiler does not track it: its waitcnt pass would otherwise wait for every
+// in-flight LDS DMA before each ds_read_b64_tr_b16 (it cannot prove they touch
+// different buffers), serialising the prefetch with the compute that should
+// hide it. Completion is ordered explicitly instead: wait_vmem() and a
+// workgroup barrier before a staged tile is read, a barrier before a stage is
+// overwritten. Untracked vector-memory operations only make the compiler's
+// own vmcnt waits more conservative, never less.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_byte_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(gptr), "s"(lds_byte_addr)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Issue the direct global->LDS loads of one 32 x D tile (one wave). Rows at or
+// beyond nvalid are replaced by row nvalid - 1: every consumer masks them (P = 0),
+// so they only need to hold finite data.
+template <typename T, int D>
+__device__ __forceinline__ void tile_load_lds(T* lds_tile, const T* __restrict__ rows, long row_stride,
+                                              int nvalid, int lane) {
+  typedef SwzTile<T, D> G;
+  const int p = lane % G::kChunks;
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds_tile));
+#pragma unroll
+  for (int t = 0; t < G::kLoads; ++t) {
+    const int row = t * G::kRowsPerLoad + lane / G::kChunks;
+    const int src_row = min(row, nvalid - 1);
+    const char* src = reinterpret_cast<const char*>(rows + (long)src_row * row_stride) + 16 * phys_chunk(row, p);
+    dma16(src, base + 1024 * t);
+  }
+}
+
+// Operand contracting over columns: lane (n, g) gets row n, columns 16 ks + 8 g .. +7.
+template <typename T, int D>
+__device__ __forceinline__ V8<T> frag_row_swz(const T* tile, int n, int g, int ks) {
+  const T* row = tile + n * D;
+  if constexpr (sizeof(T) == 2) {
+    return *reinterpret_cast<const V8<T>*>(row + 8 * phys_chunk(n, 2 * ks + g));
+  } else {
+    const V4<T> a = *reinterpret_cast<const V4<T>*>(row + 4 * phys_chunk(n, 4 * ks + 2 * g));
+    const V4<T> b = *reinterpret_cast<const V4<T>*>(row + 4 * phys_chunk(n, 4 * ks + 2 * g + 1));
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  }
+}
+
+// Operand contracting over the 32 tile rows in the permuted order of a C tile
+// fed back as an operand: lane l gets column dbase + (l & 31), rows
+// cperm(s, g, 0..7) = 16 s + 4 g + {0..3, 8..11}. For 2-byte types this is two
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4
+// of the 8 bytes that lane 4 e + i / 4 addresses, so lane i addresses columns
+// 4 (i % 4) .. +3 of row i / 4 of the 4-row block.
+template <typename T, int D>
+__device__ __forceinline__ V8<T> frag_tr_swz(const T* tile, int dbase, int lane, int s) {
+  const int g = lane >> 5;
+  if constexpr (sizeof(T) == 2) {
+    const int i = lane & 15;
+    const int d = dbase + 16 * ((lane >> 4) & 1) + 4 * (i & 3);
+    const int row = 16 * s + 4 * g + (i >> 2);
+    const int c = d >> 3, within = d & 7;
+    const T* a = tile + row * D + 8 * phys_chunk(row, c) + within;
+    const T* b = tile + (row + 8) * D + 8 * phys_chunk(row + 8, c) + within;
+    const i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a));
+    const i16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(b));
+    const V4<T> xa = __builtin_bit_cast(V4<T>, x);
+    const V4<T> yb = __builtin_bit_cast(V4<T>, y);
+    return __builtin_shufflevector(xa, yb, 0, 1, 2, 3, 4, 5, 6, 7);
+  } else {
+    const int col = dbase + (lane & 31);
+    V8<T> v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int row = 16 * s + 8 * (e >> 2) + 4 * g + (e & 3);
+      v[e] = tile[row * D + 4 * phys_chunk(row, col >> 2) + (col & 3)];
+    }
+    return v;
+  }
+}
+
+// Wait until this wave's outstanding vector-memory operations (including
+// global_load_lds) have completed; lgkm and exp counters are left alone.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// ---------------------------------------------------------------------------
 // Grid mapping. Workgroups are dispatched round-robin over the 8 XCDs of an
 // MI355X, each with its own L2. Blocks that read the same (batch, head) stream
 // are therefore remapped onto one XCD, in order, so that their shared K/V (or
