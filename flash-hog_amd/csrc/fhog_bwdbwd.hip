@@ -14,16 +14,30 @@
 // over the keys: B = r1 - dD r2 - D dD + r3 with r1 = rowsum(dPa P),
 // r2 = rowsum(dP P), r3 = rowsum(dP ddS P), which is rowsum(dP2 P) expanded.
 //
+// Element-wise form used by passes 3 and 4. With u = dP - D and t = ddS - dD,
+//   dP2 - B = dPa + u t - (D dD + B)
+// (substitute ddS = t + dD in dP2), so per (query, key) pair
+//   dS = scale P u,  dS2 = scale P (dPa + u t - c),  ddP = P t,  c = D dD + B,
+// and the common factor `scale` of dS and dS2 is applied once to the dQ2 / dK2
+// accumulators instead of per element.
+//
 // Stage 1 (passes 1-3): a workgroup owns 128 queries (4 waves x 32) of one
-// (batch, head) and streams 32-key tiles of K, V, ddK, ddV through LDS twice.
-// Score tiles are computed transposed (S^T = K Q^T) so each lane holds one
-// query row: row statistics are per-lane scalars and row sums need one
+// (batch, head) and streams 32-key tiles of K, V, ddK, ddV through an LDS ring
+// twice. Score tiles are computed transposed (S^T = K Q^T) so each lane holds
+// one query row: row statistics are per-lane scalars and row sums need one
 // cross-group add at the end of the sweep. The query-side operands stay in
 // registers for the whole sweep.
 //
 // Stage 2 (pass 4): a workgroup owns 128 keys (4 waves x 32) and streams
-// 32-query tiles of Q, dO, ddQ plus their row statistics through LDS. Score
-// tiles are S = Q K^T, so each lane holds one key column.
+// 32-query tiles of Q, dO, ddQ plus their row statistics through an LDS ring.
+// Score tiles are S = Q K^T, so each lane holds one key column.
+//
+// Causal blocks differ in length (query block r sees r + 1 key blocks), so
+// both grids issue their blocks longest first: block id -> rank = id / (B H),
+// (batch, head) = id % (B H). Workgroups are dispatched round-robin over the
+// 8 XCDs (each with its own L2); with B H a multiple of 8, XCD x then receives
+// the same eighth of the (batch, head) pairs at every rank, so the blocks that
+// stream one (batch, head) share one L2.
 #include "fhog_device.h"
 #include "fhog_params.h"
 
@@ -41,16 +55,38 @@ template <typename T, int D> struct Occupancy {
   static constexpr int value = (sizeof(T) == 2 && D == 64) ? 2 : 1;
 };
 
+// Depth of the LDS ring: tiles stream NST - 1 iterations ahead of their use.
+template <typename T, int D> struct Ring {
+  static constexpr int value = (sizeof(T) == 2 && D == 64) ? 3 : 2;
+};
+
+// Waits until the tile of iteration `it` (of `total`) has landed in LDS: the
+// loads of at most NST - 2 later tiles may still be in flight.
+template <int NST, int LOADS>
+__device__ __forceinline__ void wait_tile(int it, int total) {
+  if constexpr (NST >= 3) {
+    if (it + NST - 2 < total) {
+      wait_vmem_le<(NST - 2) * LOADS>();
+      return;
+    }
+  }
+  wait_vmem_le<0>();
+}
+
+__device__ __forceinline__ uint32_t lds_base_u32(const void* p) {
+  return __builtin_amdgcn_readfirstlane(lds_addr(p));
+}
+
 // ----------------------------------------------------------------------------
 // Stage 1: passes 1-3, tiled over queries.
 //
 // Sweep 1 (passes 1+2) computes S, ddS, dP and, per row, dD = sum ddS P,
-// r2 = sum dP P, r3 = sum dP ddS P, and accumulates u = P ddV into the ddO
-// accumulator; then r1 = sum_j P dPa = <dO_i, u_i> and
+// r2 = sum dP P, r3 = sum dP ddS P, and accumulates P ddV into the ddO
+// accumulator; then r1 = sum_j P dPa = <dO_i, (P ddV)_i> and
 // B = r1 - dD r2 - D dD + r3. Sweep 2 (pass 3) recomputes S, ddS, dP, dPa and
 // adds dS ddK + dS2 K to dQ2 and ddP V to ddO (whose P ddV part came from
-// sweep 1). Key-side tiles go global -> LDS directly (no registers) into a
-// two-stage ring with one barrier per tile.
+// sweep 1). Wave w streams key-side tensor w (K, V, ddK, ddV) global -> LDS,
+// without registers, into an NST-deep ring with one barrier per tile.
 // ----------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL>
 __global__ void __launch_bounds__(kThreads)
@@ -61,15 +97,19 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   constexpr int DT = D / 32;       // 32-wide output column blocks
   constexpr int BQ = 32 * kWaves;  // queries per workgroup
   constexpr int BK = 32;           // keys per streamed tile
-  // [stage][tensor]: 0 = K, 1 = V, 2 = ddK, 3 = ddV
-  __shared__ __attribute__((aligned(1024))) T s_kv[2][4][G::kElems];
+  constexpr int NST = Ring<T, D>::value;
+  constexpr int kTile = G::kElems * (int)sizeof(T);
+  constexpr int kStage = 4 * kTile;  // K, V, ddK, ddV
+  __shared__ __attribute__((aligned(1024))) char s_kv[NST * kStage];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, g = lane >> 5;
   const int nqb = (p.nq + BQ - 1) / BQ;
-  const int lin = xcd_remap(blockIdx.x, nqb * p.batch * p.heads);
-  const int bh = lin / nqb;
-  const int qb = CAUSAL ? nqb - 1 - lin % nqb : lin % nqb;  // longest rows first
+  const int nbh = p.batch * p.heads;
+  const int rank = blockIdx.x / nbh;
+  const int bh = blockIdx.x - rank * nbh;
+  const int qb = CAUSAL ? nqb - 1 - rank : rank;
   const int b = bh / p.heads, h = bh % p.heads;
   const long rs = (long)p.heads * D;
   const long qbase = ((long)b * p.nq * p.heads + h) * D;
@@ -102,7 +142,6 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   const float c2 = scale * kLog2e;
   const float Di = xgroup_sum(dpart);
   const float nL2 = qvalid ? -p.lse[sbase + qi] * kLog2e : 0.f;
-  const float nsD = -scale * Di;
 
   int kend = p.nk;
   if (CAUSAL) kend = min(kend, qb * BQ + BQ);
@@ -111,35 +150,59 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   if (CAUSAL) wend = min(wend, q0 + 32);
   const int wkt = q0 < p.nq ? (wend + BK - 1) / BK : 0;  // tiles with work for this wave
 
-  const T* src = (wave == 0 ? p.k : wave == 1 ? p.v : wave == 2 ? p.ddk : p.ddv) + kbase;
-  const int total = 2 * nkt;
-  tile_load_lds<T, D>(s_kv[0][wave], src, rs, p.nk, lane);
+  SwzFrags<T, D> fr;
+  fr.init(lane);
 
-  // Waits for tile `it`, then starts streaming tile it + 1 (the key sequence is
-  // streamed twice) into the other stage.
-  auto advance = [&](int it) {
-    wait_vmem();
-    __syncthreads();
-    if (it + 1 < total) {
-      const int kn = it + 1 < nkt ? it + 1 : it + 1 - nkt;
-      tile_load_lds<T, D>(s_kv[(it + 1) & 1][wave], src + (long)kn * BK * rs, rs, p.nk - kn * BK, lane);
+  // Wave w streams tensor w; the key sequence is streamed twice (iterations
+  // 0 .. nkt-1 and nkt .. 2 nkt - 1).
+  const T* src = (wave == 0 ? p.k : wave == 1 ? p.v : wave == 2 ? p.ddk : p.ddv) + kbase;
+  const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
+  TileDma<T, D> dma;
+  dma.init(row_bytes, BK, lane);
+  const uint32_t lds_wave = lds_base_u32(s_kv) + wave * kTile;
+  const int total = 2 * nkt;
+  // Retire the query-side loads here: otherwise the compiler waits for them at
+  // their first use inside the loop, and that wait (vmcnt counts every vector
+  // load, including the untracked LDS DMAs) would drain the prefetched tiles on
+  // every iteration.
+  wait_vmem();
+  auto issue = [&](int it) {
+    const int kt = it < nkt ? it : it - nkt;
+    const int nvalid = p.nk - kt * BK;
+    const uint32_t dst = lds_wave + (uint32_t)((it % NST) * kStage);
+    const T* gsrc = src + (long)kt * BK * rs;
+    if (nvalid >= BK) {
+      dma.issue(dst, gsrc);
+    } else {
+      TileDma<T, D> part;
+      part.init(row_bytes, nvalid, lane);
+      part.issue(dst, gsrc);
     }
   };
-  // P of the tile at stage `buf` (key tile kt), masked on diagonal / ragged tiles.
-  auto probs = [&](const f32x16& S, int kt) {
+#pragma unroll
+  for (int i = 0; i < NST - 1; ++i)
+    if (i < total) issue(i);
+
+  // Waits for tile `it`, then starts streaming tile it + NST - 1 into the stage
+  // every wave finished reading in the previous iteration.
+  auto advance = [&](int it) {
+    wait_tile<NST, G::kLoads>(it, total);
+    __syncthreads();
+    if (it + NST - 1 < total) issue(it + NST - 1);
+  };
+  // Masks P on a diagonal or ragged tile (uniform branch).
+  auto mask_probs = [&](f32x16& P, int kt) {
     const int k0 = kt * BK;
     const bool need_mask = (k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0);
-    const int klim = min(p.nk - 1, CAUSAL ? qi : p.nk - 1) - k0;  // last visible key, tile-relative
-    f32x16 P;
+    if (need_mask) {
+      const int klim = min(p.nk - 1, CAUSAL ? qi : p.nk - 1) - k0;  // last visible key, tile-relative
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float pv = exp2_fast(fmaf(S[r], c2, nL2));
-      P[r] = (need_mask && crow(r, g) > klim) ? 0.f : pv;
+      for (int r = 0; r < 16; ++r)
+        if (crow(r, g) > klim) P[r] = 0.f;
     }
-    return P;
   };
 
-  // ---- sweep 1: dD, r2, r3 and u = P ddV (into acc_ddo) ----
+  // ---- sweep 1: dD, r2, r3 and P ddV (into acc_ddo) ----
   f32x16 acc_ddo[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc_ddo[dt] = zero16();
@@ -147,37 +210,41 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   for (int it = 0; it < nkt; ++it) {
     advance(it);
     if (it < wkt) {
-      const T* sK = s_kv[it & 1][0];
-      const T* sV = s_kv[it & 1][1];
-      const T* sdK = s_kv[it & 1][2];
-      const T* sdV = s_kv[it & 1][3];
+      const char* st = s_kv + (it % NST) * kStage;
+      const char* sK = st;
+      const char* sV = st + kTile;
+      const char* sdK = st + 2 * kTile;
+      const char* sdV = st + 3 * kTile;
       f32x16 S = zero16(), ddS = zero16(), dP = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const V8<T> kf = frag_row_swz<T, D>(sK, n, g, ks);
+        const V8<T> kf = fr.rowf(sK, ks);
         S = mma<T>(kf, qf[ks], S);
         ddS = mma<T>(kf, ddqf[ks], ddS);
-        ddS = mma<T>(frag_row_swz<T, D>(sdK, n, g, ks), qf[ks], ddS);
-        dP = mma<T>(frag_row_swz<T, D>(sV, n, g, ks), dof[ks], dP);
+        ddS = mma<T>(fr.rowf(sdK, ks), qf[ks], ddS);
+        dP = mma<T>(fr.rowf(sV, ks), dof[ks], dP);
       }
-      const f32x16 P = probs(S, it);
+      f32x16 P;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) P[r] = exp2_fast(fmaf(S[r], c2, nL2));
+      mask_probs(P, it);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        dd_acc = fmaf(ddS[r], P[r], dd_acc);
+        const float x = ddS[r] * P[r];
+        dd_acc += x;
+        r3 = fmaf(dP[r], x, r3);
         r2 = fmaf(dP[r], P[r], r2);
-        r3 = fmaf(dP[r] * ddS[r], P[r], r3);
       }
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const V8<T> oP = cvt8<T>(s ? hi8(P) : lo8(P));
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-          acc_ddo[dt] = mma<T>(frag_tr_swz<T, D>(sdV, 32 * dt, lane, s), oP, acc_ddo[dt]);
+        for (int dt = 0; dt < DT; ++dt) acc_ddo[dt] = mma<T>(fr.trf(sdV, dt, s), oP, acc_ddo[dt]);
       }
     }
   }
 
-  // r1 = <dO_i, u_i>: u is in the accumulator layout (lane = query, registers = columns).
+  // r1 = <dO_i, (P ddV)_i>: the accumulator holds lane = query, registers = columns.
   float r1 = 0.f;
   if (qvalid) {
     const T* dorow = p.dout + qbase + (long)qi * rs;
@@ -198,9 +265,9 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
     p.ddelta[sbase + qi] = dD;
     p.bstat[sbase + qi] = Bi;
   }
-  const float ndd = -dD, nsB = -scale * Bi;
+  const float nD = -Di, ndD = -dD, nc = -(Di * dD + Bi);
 
-  // ---- sweep 2: dQ2 += dS ddK + dS2 K, ddO += ddP V ----
+  // ---- sweep 2: dQ2 += P u ddK + P (dPa + u t - c) K (times scale at the end), ddO += P t V ----
   f32x16 acc_dq2[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc_dq2[dt] = zero16();
@@ -208,21 +275,26 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
     advance(it);
     const int kt = it - nkt;
     if (kt < wkt) {
-      const T* sK = s_kv[it & 1][0];
-      const T* sV = s_kv[it & 1][1];
-      const T* sdK = s_kv[it & 1][2];
-      const T* sdV = s_kv[it & 1][3];
+      const char* st = s_kv + (it % NST) * kStage;
+      const char* sK = st;
+      const char* sV = st + kTile;
+      const char* sdK = st + 2 * kTile;
+      const char* sdV = st + 3 * kTile;
       f32x16 S = zero16(), ddS = zero16(), dP = zero16(), dPa = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const V8<T> kf = frag_row_swz<T, D>(sK, n, g, ks);
+        const V8<T> kf = fr.rowf(sK, ks);
         S = mma<T>(kf, qf[ks], S);
         ddS = mma<T>(kf, ddqf[ks], ddS);
-        ddS = mma<T>(frag_row_swz<T, D>(sdK, n, g, ks), qf[ks], ddS);
-        dP = mma<T>(frag_row_swz<T, D>(sV, n, g, ks), dof[ks], dP);
-        dPa = mma<T>(frag_row_swz<T, D>(sdV, n, g, ks), dof[ks], dPa);
+        ddS = mma<T>(fr.rowf(sdK, ks), qf[ks], ddS);
+        const V8<T> vf = fr.rowf(sV, ks);
+        dP = mma<T>(vf, dof[ks], dP);
+        dPa = mma<T>(fr.rowf(sdV, ks), dof[ks], dPa);
       }
-      const f32x16 P = probs(S, kt);
+      f32x16 P;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) P[r] = exp2_fast(fmaf(S[r], c2, nL2));
+      mask_probs(P, kt);
       // one 16-key half at a time: compute, convert, multiply
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
@@ -230,21 +302,21 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int r = 8 * s + e;
-          const float t = fmaf(ddS[r], scale, ndd);            // ddS - dD
-          float w = fmaf(dP[r], t, dPa[r]);                     // dPa + dP (ddS - dD)
-          w = fmaf(ddS[r], nsD, w);                             //   - ddS D  = dP2
-          vdS[e] = P[r] * fmaf(dP[r], scale, nsD);              // scale P (dP - D)
-          vdS2[e] = P[r] * fmaf(w, scale, nsB);                 // scale P (dP2 - B)
-          vddP[e] = P[r] * t;                                   // P (ddS - dD)
+          const float u = dP[r] + nD;                   // dP - D
+          const float t = fmaf(ddS[r], scale, ndD);     // ddS - dD
+          const float x = fmaf(u, t, dPa[r]) + nc;      // dP2 - B
+          vdS[e] = P[r] * u;
+          vdS2[e] = P[r] * x;
+          vddP[e] = P[r] * t;
         }
         const V8<T> oS = cvt8<T>(vdS);
         const V8<T> oS2 = cvt8<T>(vdS2);
         const V8<T> odP = cvt8<T>(vddP);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          acc_dq2[dt] = mma<T>(frag_tr_swz<T, D>(sdK, 32 * dt, lane, s), oS, acc_dq2[dt]);
-          acc_dq2[dt] = mma<T>(frag_tr_swz<T, D>(sK, 32 * dt, lane, s), oS2, acc_dq2[dt]);
-          acc_ddo[dt] = mma<T>(frag_tr_swz<T, D>(sV, 32 * dt, lane, s), odP, acc_ddo[dt]);
+          acc_dq2[dt] = mma<T>(fr.trf(sdK, dt, s), oS, acc_dq2[dt]);
+          acc_dq2[dt] = mma<T>(fr.trf(sK, dt, s), oS2, acc_dq2[dt]);
+          acc_ddo[dt] = mma<T>(fr.trf(sV, dt, s), odP, acc_ddo[dt]);
         }
       }
     }
@@ -261,7 +333,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
         f32x4 x, y;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          x[j] = acc_dq2[dt][4 * a + j];
+          x[j] = acc_dq2[dt][4 * a + j] * scale;
           y[j] = acc_ddo[dt][4 * a + j];
         }
         *reinterpret_cast<V4<T>*>(dq2 + d) = cvt4<T>(x);
@@ -272,9 +344,11 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
 }
 
 // ----------------------------------------------------------------------------
-// Stage 2: pass 4, tiled over keys. Query-side tiles (Q, dO, ddQ) go
-// global -> LDS directly; the four row statistics of each query tile are
-// staged through registers as -L log2(e), -scale D, -dD, -scale B.
+// Stage 2: pass 4, tiled over keys. Waves 0-2 stream the query-side tiles
+// (Q, dO, ddQ) global -> LDS; wave 3 streams the tiles' row statistics and
+// turns them into the four per-query constants (-L log2(e), -D, -dD,
+// -(D dD + B)) in LDS. The loop issues no load the compiler tracks, so its
+// only vector-memory waits are the explicit ones.
 // ----------------------------------------------------------------------------
 template <typename T, int D, bool CAUSAL>
 __global__ void __launch_bounds__(kThreads)
@@ -285,16 +359,18 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
   constexpr int DT = D / 32;
   constexpr int BKB = 32 * kWaves;  // keys per workgroup
   constexpr int BQ = 32;            // queries per streamed tile
-  // [stage][tensor]: 0 = Q, 1 = dO, 2 = ddQ
-  __shared__ __attribute__((aligned(1024))) T s_q[2][3][G::kElems];
-  __shared__ __attribute__((aligned(16))) float s_stat[2][4][BQ];
+  constexpr int NST = Ring<T, D>::value;
+  constexpr int kTile = G::kElems * (int)sizeof(T);
+  constexpr int kStat = 4 * BQ * (int)sizeof(float);
+  constexpr int kStage = 3 * kTile + kStat;  // Q, dO, ddQ, constants
+  __shared__ __attribute__((aligned(1024))) char s_q[NST * kStage];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, g = lane >> 5;
-  const int nkb = (p.nk + BKB - 1) / BKB;
-  const int lin = xcd_remap(blockIdx.x, nkb * p.batch * p.heads);
-  const int bh = lin / nkb;
-  const int kb = lin % nkb;  // causal: the longest key columns come first
+  const int nbh = p.batch * p.heads;
+  const int kb = blockIdx.x / nbh;  // causal: the longest key columns come first
+  const int bh = blockIdx.x - kb * nbh;
   const int b = bh / p.heads, h = bh % p.heads;
   const long rs = (long)p.heads * D;
   const long qbase = ((long)b * p.nq * p.heads + h) * D;
@@ -335,93 +411,167 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
     const float scale = p.scale;
     const float c2 = scale * kLog2e;
 
-    // Wave w streams query-side tensor w (w < 3); every wave stages statistic w.
-    const T* src = (wave == 0 ? p.q : wave == 1 ? p.dout : p.ddq) + qbase;
-    const float* st_src = (wave == 0 ? p.lse : wave == 1 ? p.delta : wave == 2 ? p.ddelta : p.bstat) + sbase;
-    const float st_mul = wave == 0 ? -kLog2e : wave == 1 ? -scale : wave == 2 ? -1.f : -scale;
-    auto load_stat = [&](int qt) {
-      const int q = qt * BQ + n;
-      return (g == 0 && q < p.nq) ? st_src[q] * st_mul : 0.f;
-    };
+    SwzFrags<T, D> fr;
+    fr.init(lane);
 
-    if (wave < 3) tile_load_lds<T, D>(s_q[0][wave], src + (long)qt_begin * BQ * rs, rs, p.nq - qt_begin * BQ, lane);
-    {
-      const float v = load_stat(qt_begin);
-      if (g == 0) s_stat[0][wave][n] = v;
+    const int total = nqt - qt_begin;
+    // Retire the key-side loads before the ring starts (see bwdbwd_q_kernel).
+    wait_vmem();
+    const T* src = (wave == 0 ? p.q : wave == 1 ? p.dout : p.ddq) + qbase;
+    const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
+    TileDma<T, D> dma;
+    dma.init(row_bytes, BQ, lane);
+    const uint32_t lds_wave = lds_base_u32(s_q) + wave * kTile;
+
+    // Wave 3 streams the per-query statistics of each tile with two dword DMAs
+    // (lanes 0-31 then 32-63: L and D, then dD and B; rows past nq repeat row
+    // nq - 1) into the tile's stage, and once they have landed rewrites them in
+    // place as the initial values of the four score accumulators:
+    // -L / scale, -dD / scale, -D, -(D dD + B).
+    constexpr int kStatLoads = 2;
+    auto issue_stats = [&](int i) {
+      const int q = min((qt_begin + i) * BQ + n, p.nq - 1);
+      const uint32_t dst = lds_base_u32(s_q) + (uint32_t)((i % NST) * kStage + 3 * kTile);
+      dma4((g ? p.delta : p.lse) + sbase + q, dst);
+      dma4((g ? p.bstat : p.ddelta) + sbase + q, dst + 256);
+    };
+    const float inv_scale = 1.0f / scale;
+    auto finish_stats = [&](int i) {
+      if (g == 0) {
+        float* st = reinterpret_cast<float*>(s_q + (i % NST) * kStage + 3 * kTile);
+        const float L = st[n], Dq = st[BQ + n], dDq = st[2 * BQ + n], Bq = st[3 * BQ + n];
+        st[n] = -L * inv_scale;
+        st[BQ + n] = -dDq * inv_scale;
+        st[2 * BQ + n] = -Dq;
+        st[3 * BQ + n] = -fmaf(Dq, dDq, Bq);
+      }
+    };
+    // Waits (wave 3) until the statistics of tile i have landed: the DMAs of
+    // later tiles, at most NST - 2 of them, may still be in flight.
+    auto wait_stats = [&](int i) {
+      if constexpr (NST >= 3) {
+        if (i + NST - 2 < total) {
+          wait_vmem_le<(NST - 2) * kStatLoads>();
+          return;
+        }
+      }
+      wait_vmem_le<0>();
+    };
+    auto issue = [&](int i) {
+      if (wave == 3) {
+        issue_stats(i);
+        return;
+      }
+      const int q0t = (qt_begin + i) * BQ;
+      const int nvalid = p.nq - q0t;
+      const uint32_t dst = lds_wave + (uint32_t)((i % NST) * kStage);
+      const T* gsrc = src + (long)q0t * rs;
+      if (nvalid >= BQ) {
+        dma.issue(dst, gsrc);
+      } else {
+        TileDma<T, D> part;
+        part.init(row_bytes, nvalid, lane);
+        part.issue(dst, gsrc);
+      }
+    };
+#pragma unroll
+    for (int i = 0; i < NST - 1; ++i)
+      if (i < total) issue(i);
+    if (wave == 3) {
+      wait_stats(0);
+      finish_stats(0);
     }
 
-    for (int qt = qt_begin; qt < nqt; ++qt) {
-      const int buf = (qt - qt_begin) & 1;
-      const bool has_next = qt + 1 < nqt;
-      wait_vmem();
+    for (int i = 0; i < total; ++i) {
+      if (wave < 3) wait_tile<NST, G::kLoads>(i, total);
       __syncthreads();
-      float st_next = 0.f;
-      if (has_next) {
-        st_next = load_stat(qt + 1);
-        if (wave < 3)
-          tile_load_lds<T, D>(s_q[buf ^ 1][wave], src + (long)(qt + 1) * BQ * rs, rs, p.nq - (qt + 1) * BQ, lane);
-      }
+      if (i + NST - 1 < total) issue(i + NST - 1);
+      const int qt = qt_begin + i;
       const int q0 = qt * BQ;
       const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0);
       if (active) {
-        const T* sQ = s_q[buf][0];
-        const T* sdO = s_q[buf][1];
-        const T* sdQ = s_q[buf][2];
-        f32x16 S = zero16(), ddS = zero16(), dP = zero16(), dPa = zero16();
+        const char* st = s_q + (i % NST) * kStage;
+        const char* sQ = st;
+        const char* sdO = st + kTile;
+        const char* sdQ = st + 2 * kTile;
+        const float* sc = reinterpret_cast<const float*>(st + 3 * kTile);
+        // The accumulators start at the per-query constants (register r holds
+        // query 8 (r / 4) + 4 g + r % 4 of the tile), so they end as
+        //   S' = S_raw - L / scale, ddS' = ddS_raw - dD / scale,
+        //   u = dP - D, dPa' = dPa - (D dD + B).
+        f32x16 S, ddS, dP, dPa;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          const int m0 = 8 * a + 4 * g;
+          const f32x4 c0 = *reinterpret_cast<const f32x4*>(sc + m0);
+          const f32x4 c1 = *reinterpret_cast<const f32x4*>(sc + BQ + m0);
+          const f32x4 c2v = *reinterpret_cast<const f32x4*>(sc + 2 * BQ + m0);
+          const f32x4 c3 = *reinterpret_cast<const f32x4*>(sc + 3 * BQ + m0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            S[4 * a + j] = c0[j];
+            ddS[4 * a + j] = c1[j];
+            dP[4 * a + j] = c2v[j];
+            dPa[4 * a + j] = c3[j];
+          }
+        }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const V8<T> qa = frag_row_swz<T, D>(sQ, n, g, ks);
-          const V8<T> dqa = frag_row_swz<T, D>(sdQ, n, g, ks);
-          const V8<T> doa = frag_row_swz<T, D>(sdO, n, g, ks);
+          const V8<T> qa = fr.rowf(sQ, ks);
+          const V8<T> dqa = fr.rowf(sdQ, ks);
+          const V8<T> doa = fr.rowf(sdO, ks);
           S = mma<T>(qa, kf[ks], S);
           ddS = mma<T>(dqa, kf[ks], ddS);
           ddS = mma<T>(qa, dkf[ks], ddS);
           dP = mma<T>(doa, vf[ks], dP);
           dPa = mma<T>(doa, dvf[ks], dPa);
         }
+        f32x16 P;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) P[r] = exp2_fast(S[r] * c2);
         const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31);
-        // visible iff query >= qmin (causal) and query < nq
-        const int qlo = (CAUSAL ? kj : 0) - q0, qhi = p.nq - q0;
+        if (need_mask) {
+          // visible iff query >= key (causal) and query < nq
+          const int qlo = (CAUSAL ? kj : 0) - q0, qhi = p.nq - q0;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = crow(r, g);
+            if (m < qlo || m >= qhi) P[r] = 0.f;
+          }
+        }
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
           f32x8 vdS, vdS2, vddP;
 #pragma unroll
-          for (int ah = 0; ah < 2; ++ah) {
-            const int a = 2 * s + ah;
-            const int m0 = 8 * a + 4 * g;
-            const f32x4 nl2 = *reinterpret_cast<const f32x4*>(&s_stat[buf][0][m0]);
-            const f32x4 nsd = *reinterpret_cast<const f32x4*>(&s_stat[buf][1][m0]);
-            const f32x4 ndd = *reinterpret_cast<const f32x4*>(&s_stat[buf][2][m0]);
-            const f32x4 nsb = *reinterpret_cast<const f32x4*>(&s_stat[buf][3][m0]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int r = 4 * a + j, e = 4 * ah + j;
-              float pv = exp2_fast(fmaf(S[r], c2, nl2[j]));
-              if (need_mask) pv = (m0 + j < qlo || m0 + j >= qhi) ? 0.f : pv;
-              const float t = fmaf(ddS[r], scale, ndd[j]);
-              float w = fmaf(dP[r], t, dPa[r]);
-              w = fmaf(ddS[r], nsd[j], w);
-              vdS[e] = pv * fmaf(dP[r], scale, nsd[j]);
-              vdS2[e] = pv * fmaf(w, scale, nsb[j]);
-              vddP[e] = pv * t;
-            }
+          for (int e = 0; e < 8; ++e) {
+            const int r = 8 * s + e;
+            const float t = ddS[r] * scale;              // ddS - dD
+            const float x = fmaf(dP[r], t, dPa[r]);      // dP2 - B
+            vdS[e] = P[r] * dP[r];
+            vdS2[e] = P[r] * x;
+            vddP[e] = P[r] * t;
           }
           const V8<T> oS = cvt8<T>(vdS);
           const V8<T> oS2 = cvt8<T>(vdS2);
           const V8<T> odP = cvt8<T>(vddP);
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
-            acc_dk2[dt] = mma<T>(frag_tr_swz<T, D>(sdQ, 32 * dt, lane, s), oS, acc_dk2[dt]);
-            acc_dk2[dt] = mma<T>(frag_tr_swz<T, D>(sQ, 32 * dt, lane, s), oS2, acc_dk2[dt]);
-            acc_dv2[dt] = mma<T>(frag_tr_swz<T, D>(sdO, 32 * dt, lane, s), odP, acc_dv2[dt]);
+            acc_dk2[dt] = mma<T>(fr.trf(sdQ, dt, s), oS, acc_dk2[dt]);
+            acc_dk2[dt] = mma<T>(fr.trf(sQ, dt, s), oS2, acc_dk2[dt]);
+            acc_dv2[dt] = mma<T>(fr.trf(sdO, dt, s), odP, acc_dv2[dt]);
           }
         }
       }
-      if (has_next && g == 0) s_stat[buf ^ 1][wave][n] = st_next;
+      // Tile i + 1's statistics are read after the next barrier.
+      if (wave == 3 && i + 1 < total) {
+        wait_stats(i + 1);
+        finish_stats(i + 1);
+      }
     }
   }
 
   if (kvalid) {
+    const float scale = p.scale;
     T* dk2 = p.dk2 + kbase + (long)kj * rs;
     T* dv2 = p.dv2 + kbase + (long)kj * rs;
 #pragma unroll
@@ -432,7 +582,7 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
         f32x4 x, y;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          x[j] = acc_dk2[dt][4 * a + j];
+          x[j] = acc_dk2[dt][4 * a + j] * scale;
           y[j] = acc_dv2[dt][4 * a + j];
         }
         *reinterpret_cast<V4<T>*>(dk2 + d) = cvt4<T>(x);

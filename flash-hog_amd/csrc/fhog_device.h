@@ -300,6 +300,113 @@ __device__ __forceinline__ V8<T> frag_tr_swz(const T* tile, int dbase, int lane,
 // global_load_lds) have completed; lgkm and exp counters are left alone.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (s_waitcnt encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+// Loads complete in issue order for this counter, so after the wait every load
+// issued before the last N has landed.
+template <int N> __device__ __forceinline__ void wait_vmem_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// One wave-wide 16-byte-per-lane global -> LDS load addressed as a uniform
+// 64-bit base (SGPR pair) plus a per-lane 32-bit byte offset; lane l's 16 bytes
+// land at lds_byte_addr + 16 l. Untracked by the compiler for the same reason
+// as dma16.
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds_byte_addr)
+               : "memory", "m0");
+}
+
+// One wave-wide 4-byte-per-lane global -> LDS load: lane l's dword at gptr
+// lands at lds_byte_addr + 4 l. Untracked by the compiler (see dma16).
+__device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_byte_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :
+               : "v"(gptr), "s"(lds_byte_addr)
+               : "memory", "m0");
+}
+
+// Per-lane source offsets of the wave-wide loads that fill one swizzled 32 x D
+// tile (same placement as tile_load_lds). They depend only on the lane, the
+// row stride and the number of valid rows, so a streaming loop computes them
+// once and then only advances the uniform base address per tile.
+template <typename T, int D> struct TileDma {
+  typedef SwzTile<T, D> G;
+  uint32_t voff[G::kLoads];
+
+  // Rows at or beyond nvalid are redirected to row nvalid - 1 (finite data for
+  // rows that every consumer masks).
+  __device__ __forceinline__ void init(uint32_t row_stride_bytes, int nvalid, int lane) {
+    const int p = lane % G::kChunks;
+#pragma unroll
+    for (int t = 0; t < G::kLoads; ++t) {
+      const int row = t * G::kRowsPerLoad + lane / G::kChunks;
+      const int src_row = min(row, nvalid - 1);
+      voff[t] = (uint32_t)src_row * row_stride_bytes + 16u * (uint32_t)phys_chunk(row, p);
+    }
+  }
+
+  // lds_byte_addr must be wave-uniform; gbase is the tile's first row.
+  __device__ __forceinline__ void issue(uint32_t lds_byte_addr, const void* gbase) const {
+#pragma unroll
+    for (int t = 0; t < G::kLoads; ++t) dma16s(gbase, voff[t], lds_byte_addr + 1024u * t);
+  }
+};
+
+// Per-lane byte offsets of the MFMA operand fragments read from a swizzled
+// 32 x D tile (frag_row_swz / frag_tr_swz), computed once per kernel so that
+// each read is one address add of the tile base plus an immediate offset.
+template <typename T, int D> struct SwzFrags {
+  uint32_t row[D / 16];  // row operand of step ks
+  uint32_t tr[D / 32];   // first transposed read of column block dt, step s = 0
+  int lane;
+
+  __device__ __forceinline__ void init(int lane_id) {
+    lane = lane_id;
+    if constexpr (sizeof(T) == 2) {
+      const int n = lane & 31, g = lane >> 5;
+#pragma unroll
+      for (int ks = 0; ks < D / 16; ++ks)
+        row[ks] = 2u * (uint32_t)(n * D + 8 * phys_chunk(n, 2 * ks + g));
+      const int i = lane & 15;
+      const int row0 = 4 * g + (i >> 2);
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const int d = 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (i & 3);
+        tr[dt] = 2u * (uint32_t)(row0 * D + 8 * phys_chunk(row0, d >> 3) + (d & 7));
+      }
+    }
+  }
+
+  // Operand contracting over columns: lane (n, g) gets row n, columns 16 ks + 8 g .. +7.
+  __device__ __forceinline__ V8<T> rowf(const char* tile, int ks) const {
+    if constexpr (sizeof(T) == 2) {
+      return *reinterpret_cast<const V8<T>*>(tile + row[ks]);
+    } else {
+      return frag_row_swz<T, D>(reinterpret_cast<const T*>(tile), lane & 31, lane >> 5, ks);
+    }
+  }
+
+  // Operand contracting over the tile rows in the permuted C order (frag_tr_swz):
+  // rows 16 s + 4 g + {0..3} and the same + 8 share the swizzle of rows 4 g + {0..3}
+  // (the swizzle repeats every 8 rows), so both reads are fixed offsets from tr[dt].
+  __device__ __forceinline__ V8<T> trf(const char* tile, int dt, int s) const {
+    if constexpr (sizeof(T) == 2) {
+      const char* a = tile + tr[dt] + s * 32 * D;
+      const i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a));
+      const i16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a + 16 * D));
+      const V4<T> xa = __builtin_bit_cast(V4<T>, x);
+      const V4<T> yb = __builtin_bit_cast(V4<T>, y);
+      return __builtin_shufflevector(xa, yb, 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      return frag_tr_swz<T, D>(reinterpret_cast<const T*>(tile), 32 * dt, lane, s);
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // Grid mapping. Workgroups are dispatched round-robin over the 8 XCDs of an
 // MI355X, each with its own L2. Blocks that read the same (batch, head) stream
