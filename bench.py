@@ -58,6 +58,23 @@ def make_inputs(torch, B, N, H, D, dtype, device, seed=0):
     return out
 
 
+# HBM bytes per launch of the stage-1 kernel, measured by two rocprofv3 PMC runs
+# of this benchmark (FETCH_SIZE, then WRITE_SIZE) and calibrated with the same
+# counters on a plain device copy of known size; written by the profiling step
+# into profiles/ (see the file for the commands).
+TRAFFIC_FILE = REPO / "profiles" / "bwdbwd_q_kernel_b4_n2048_h16_d64_bf16_causal.traffic.json"
+
+
+def stage1_traffic():
+    try:
+        t = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    fetch = t["kernel_fetch_kib"] * t["copy_read_bytes"] / t["copy_fetch_kib"]
+    write = t["kernel_write_kib"] * t["copy_write_bytes"] / t["copy_write_kib"]
+    return {"bytes": int(fetch + write), "source": TRAFFIC_FILE.name}
+
+
 def cpu_baseline(args, B, N, H, D, scale, causal):
     """The reference's CPU path restated: torch-CPU fp32 autograd double VJP of
     materialised attention (oracle/autodiff.py), one (batch, head) slice at a
@@ -190,8 +207,10 @@ def main(argv=None):
     value = alg_flops / (ms_per_step * 1e-3) / 1e12
     s1_alg = 18.0 * D * pairs
     s1_tflops = s1_alg / (s1_ms * 1e-3) / 1e12
-    # executed MFMA work: stage 1 = 14 products per streamed tile pair, stage 2 = 8
-    exec_tflops = (28.0 + 16.0) * D * pairs / (ms_per_step * 1e-3) / 1e12
+    # executed MFMA work per unmasked pair: stage 1 = 13 products (5 in sweep 1,
+    # 8 in sweep 2), stage 2 = 8 products; 2 * d flops each
+    exec_tflops = (26.0 + 16.0) * D * pairs / (ms_per_step * 1e-3) / 1e12
+    traffic = stage1_traffic()
 
     # Peak memory of one call with torch-owned outputs, against the inputs.
     torch.cuda.synchronize()
@@ -243,7 +262,9 @@ def main(argv=None):
         "pct_of_bf16_peak": round(100.0 * value / MI355X_PEAK_BF16_TFLOPS, 3),
         "roofline": {"bound": "mfma", "kernel": "bwdbwd_q_kernel (stage 1, passes 1-3)",
                      "achieved": round(s1_tflops, 3), "peak": MI355X_PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(s1_tflops / MI355X_PEAK_BF16_TFLOPS, 5), "traffic": None,
+                     "frac": round(s1_tflops / MI355X_PEAK_BF16_TFLOPS, 5),
+                     "traffic": None if traffic is None else traffic["bytes"],
+                     "traffic_source": None if traffic is None else traffic["source"],
                      "alg_flops_per_launch": s1_alg, "ms_per_launch": round(s1_ms, 5)},
         "cpu_baseline": None if cpu is None else {k: (round(v, 6) if isinstance(v, float) else v)
                                                   for k, v in cpu.items()},

@@ -329,30 +329,45 @@ __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_byte_addr) {
                : "memory", "m0");
 }
 
-// Per-lane source offsets of the wave-wide loads that fill one swizzled 32 x D
-// tile (same placement as tile_load_lds). They depend only on the lane, the
-// row stride and the number of valid rows, so a streaming loop computes them
-// once and then only advances the uniform base address per tile.
-template <typename T, int D> struct TileDma {
+// One wave-wide 4-byte-per-lane global -> LDS load addressed as a uniform base
+// plus a per-lane 32-bit byte offset; lane l's dword lands at
+// lds_byte_addr + 4 l. Untracked by the compiler (see dma16).
+__device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(lds_byte_addr)
+               : "memory", "m0");
+}
+
+// Per-lane source offsets of wave-wide loads that fill one swizzled 32 x D
+// tile (same placement as tile_load_lds): loads first .. first + COUNT - 1 of
+// the tile's kLoads (a wave may fill only part of a tile). They depend only on
+// the lane, the row stride and the number of valid rows, so a streaming loop
+// computes them once and then only advances the uniform base address per tile.
+template <typename T, int D, int COUNT = SwzTile<T, D>::kLoads> struct TileDma {
   typedef SwzTile<T, D> G;
-  uint32_t voff[G::kLoads];
+  static_assert(COUNT >= 1 && COUNT <= G::kLoads, "bad load count");
+  uint32_t voff[COUNT];
+  int first;
 
   // Rows at or beyond nvalid are redirected to row nvalid - 1 (finite data for
-  // rows that every consumer masks).
-  __device__ __forceinline__ void init(uint32_t row_stride_bytes, int nvalid, int lane) {
+  // rows that every consumer masks). first_load must be wave-uniform.
+  __device__ __forceinline__ void init(uint32_t row_stride_bytes, int nvalid, int lane, int first_load = 0) {
+    first = first_load;
     const int p = lane % G::kChunks;
 #pragma unroll
-    for (int t = 0; t < G::kLoads; ++t) {
-      const int row = t * G::kRowsPerLoad + lane / G::kChunks;
+    for (int i = 0; i < COUNT; ++i) {
+      const int row = (first + i) * G::kRowsPerLoad + lane / G::kChunks;
       const int src_row = min(row, nvalid - 1);
-      voff[t] = (uint32_t)src_row * row_stride_bytes + 16u * (uint32_t)phys_chunk(row, p);
+      voff[i] = (uint32_t)src_row * row_stride_bytes + 16u * (uint32_t)phys_chunk(row, p);
     }
   }
 
-  // lds_byte_addr must be wave-uniform; gbase is the tile's first row.
-  __device__ __forceinline__ void issue(uint32_t lds_byte_addr, const void* gbase) const {
+  // lds_tile_addr (the tile's first byte) must be wave-uniform; gbase is the
+  // tile's first row.
+  __device__ __forceinline__ void issue(uint32_t lds_tile_addr, const void* gbase) const {
 #pragma unroll
-    for (int t = 0; t < G::kLoads; ++t) dma16s(gbase, voff[t], lds_byte_addr + 1024u * t);
+    for (int i = 0; i < COUNT; ++i) dma16s(gbase, voff[i], lds_tile_addr + 1024u * (first + i));
   }
 };
 
