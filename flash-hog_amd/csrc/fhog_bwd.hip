@@ -6,11 +6,16 @@
 // flash_hog/_jax_refs/jax_impl.py:142-191 (attn_bwd).
 //
 // Kernel 1 (tiled over queries) computes D for its rows, writes it, and
-// accumulates dQ while streaming K and V. Kernel 2 (tiled over keys) reads D
-// and accumulates dK and dV while streaming Q, dO and the row statistics.
-// Score tiles use the same transposed-versus-direct orientation as the
-// double backward so that every row statistic is a per-lane scalar or a
-// 4-wide LDS read.
+// accumulates dQ while streaming K and V. Kernel 2 (tiled over keys) reads L
+// and D and accumulates dK and dV while streaming Q and dO. Both stream their
+// tiles global -> LDS (no registers) through a 3-stage ring of XOR-swizzled
+// tiles with one barrier per tile, issue causal blocks longest first with
+// (batch, head) as the minor index, mask only diagonal and ragged tiles, and
+// apply the factor `scale` of dS once to the dQ / dK accumulators. Score tiles
+// use the orientations of the double backward (fhog_bwdbwd.hip): transposed
+// in kernel 1 (row statistics are per-lane scalars), direct in kernel 2,
+// whose score accumulators start at the per-query constants -L / scale and -D
+// so that the MFMAs fold them in.
 #include "fhog_device.h"
 #include "fhog_params.h"
 
@@ -20,23 +25,37 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kStages = 3;
+
+// Waves per SIMD the register allocator is asked to allow: two for 2-byte
+// types at D = 64, one otherwise.
+template <typename T, int D> struct Occupancy {
+  static constexpr int value = (sizeof(T) == 2 && D == 64) ? 2 : 1;
+};
 
 template <typename T, int D, bool CAUSAL>
-__global__ void __launch_bounds__(kThreads) bwd_q_kernel(BwdParams<T> p) {
-  typedef TileGeom<T, D> G;
+__global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
+bwd_q_kernel(BwdParams<T> p) {
+  typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
   constexpr int BQ = 32 * kWaves;
   constexpr int BK = 32;
-  __shared__ __attribute__((aligned(32))) T s_row[2][2][G::kRowElems];  // K, V
-  __shared__ __attribute__((aligned(32))) T s_tr[2][2][G::kTrElems];
+  constexpr int NST = kStages;
+  constexpr int kTile = G::kElems * (int)sizeof(T);
+  constexpr int kStage = 2 * kTile;  // K, V
+  constexpr int kPer = G::kLoads / 2;
+  __shared__ __attribute__((aligned(1024))) char s_kv[NST * kStage];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, g = lane >> 5;
   const int nqb = (p.nq + BQ - 1) / BQ;
-  const int lin = xcd_remap(blockIdx.x, nqb * p.batch * p.heads);
-  const int bh = lin / nqb;
-  const int qb = CAUSAL ? nqb - 1 - lin % nqb : lin % nqb;
+  const int nbh = p.batch * p.heads;
+  const int rank = blockIdx.x / nbh;
+  const int bh = blockIdx.x - rank * nbh;
+  const int qb = CAUSAL ? nqb - 1 - rank : rank;
   const int b = bh / p.heads, h = bh % p.heads;
   const long rs = (long)p.heads * D;
   const long qbase = ((long)b * p.nq * p.heads + h) * D;
@@ -63,7 +82,7 @@ __global__ void __launch_bounds__(kThreads) bwd_q_kernel(BwdParams<T> p) {
     }
   }
   const float Di = xgroup_sum(dpart);
-  const float Li2 = qvalid ? p.lse[sbase + qi] * kLog2e : 0.f;
+  const float nL2 = qvalid ? -p.lse[sbase + qi] * kLog2e : 0.f;
 
   int kend = p.nk;
   if (CAUSAL) kend = min(kend, qb * BQ + BQ);
@@ -78,51 +97,65 @@ __global__ void __launch_bounds__(kThreads) bwd_q_kernel(BwdParams<T> p) {
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = zero16();
 
-  const bool loader = wave < 2;
-  const T* src = (wave == 0 ? p.k : p.v) + kbase;
-  TileRegs<T, D> pre;
-  if (loader) {
-    tile_load<T, D>(pre, src, rs, p.nk, lane);
-    tile_store_lds<T, D>(pre, s_row[0][wave], s_tr[0][wave], lane);
-  }
-  __syncthreads();
+  SwzFrags<T, D> fr;
+  fr.init(lane);
+  const int tensor = wave >> 1;  // 0 = K, 1 = V
+  const T* src = (tensor == 0 ? p.k : p.v) + kbase;
+  const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
+  TileDma<T, D, kPer> dma;
+  dma.init(row_bytes, BK, lane, kPer * (wave & 1));
+  const uint32_t lds_tensor = lds_base_u32(s_kv) + tensor * kTile;
+  auto issue = [&](int kt) {
+    const int nvalid = p.nk - kt * BK;
+    const uint32_t dst = lds_tensor + (uint32_t)((kt % NST) * kStage);
+    const T* gsrc = src + (long)kt * BK * rs;
+    if (nvalid >= BK) {
+      dma.issue(dst, gsrc);
+    } else {
+      TileDma<T, D, kPer> part;
+      part.init(row_bytes, nvalid, lane, kPer * (wave & 1));
+      part.issue(dst, gsrc);
+    }
+  };
+
+  // Retire the query-side loads before the ring starts (see fwd_kernel).
+  wait_vmem();
+#pragma unroll
+  for (int i = 0; i < NST - 1; ++i)
+    if (i < nkt) issue(i);
 
   for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    const bool has_next = kt + 1 < nkt;
-    if (has_next && loader) tile_load<T, D>(pre, src + (long)(kt + 1) * BK * rs, rs, p.nk - (kt + 1) * BK, lane);
+    wait_tile<NST, kPer>(kt, nkt);
+    __syncthreads();
+    if (kt + NST - 1 < nkt) issue(kt + NST - 1);
     if (kt < wkt) {
-      const T* sK = s_row[buf][0];
-      const T* sV = s_row[buf][1];
+      const char* st = s_kv + (kt % NST) * kStage;
       f32x16 S = zero16(), dP = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        S = mma<T>(frag_row<T, D>(sK, n, g, ks), qf[ks], S);
-        dP = mma<T>(frag_row<T, D>(sV, n, g, ks), dof[ks], dP);
+        S = mma<T>(fr.rowf(st, ks), qf[ks], S);
+        dP = mma<T>(fr.rowf(st + kTile, ks), dof[ks], dP);
       }
-      const int k0 = kt * BK;
-      const bool need_mask = (k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0);
-      f32x16 vdS;
+      f32x16 P;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = exp2_fast(S[r] * c2 - Li2);
-        if (need_mask) {
-          const int kj = k0 + crow(r, g);
-          const bool ok = kj < p.nk && (!CAUSAL || kj <= qi);
-          pv = ok ? pv : 0.f;
-        }
-        vdS[r] = pv * scale * (dP[r] - Di);
+      for (int r = 0; r < 16; ++r) P[r] = exp2_fast(fmaf(S[r], c2, nL2));
+      const int k0 = kt * BK;
+      if ((k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0)) {
+        const int klim = min(p.nk - 1, CAUSAL ? qi : p.nk - 1) - k0;  // last visible key, tile-relative
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (crow(r, g) > klim) P[r] = 0.f;
       }
-      const T* tK = s_tr[buf][0];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const V8<T> oS = cvt8<T>(s ? hi8(vdS) : lo8(vdS));
+        f32x8 vdS;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] = mma<T>(frag_tr<T, D>(tK, 32 * dt + n, g, s), oS, acc[dt]);
+        for (int e = 0; e < 8; ++e) vdS[e] = P[8 * s + e] * (dP[8 * s + e] - Di);  // dS / scale
+        const V8<T> oS = cvt8<T>(vdS);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = mma<T>(fr.trf(st, dt, s), oS, acc[dt]);
       }
     }
-    if (has_next && loader) tile_store_lds<T, D>(pre, s_row[buf ^ 1][wave], s_tr[buf ^ 1][wave], lane);
-    __syncthreads();
   }
 
   if (qvalid) {
@@ -133,7 +166,7 @@ __global__ void __launch_bounds__(kThreads) bwd_q_kernel(BwdParams<T> p) {
       for (int a = 0; a < 4; ++a) {
         f32x4 x;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) x[j] = acc[dt][4 * a + j];
+        for (int j = 0; j < 4; ++j) x[j] = acc[dt][4 * a + j] * scale;
         *reinterpret_cast<V4<T>*>(dq + 32 * dt + 8 * a + 4 * g) = cvt4<T>(x);
       }
     }
@@ -141,24 +174,36 @@ __global__ void __launch_bounds__(kThreads) bwd_q_kernel(BwdParams<T> p) {
   }
 }
 
+// Kernel 2: tiled over keys. Waves 0-1 load the two halves of each Q tile,
+// waves 2-3 those of each dO tile; wave 3 also loads the tile's L and D with
+// dword DMAs and, once they have landed, rewrites them in LDS as the initial
+// values of the S and dP accumulators (-L / scale and -D).
 template <typename T, int D, bool CAUSAL>
-__global__ void __launch_bounds__(kThreads) bwd_k_kernel(BwdParams<T> p) {
-  typedef TileGeom<T, D> G;
+__global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
+bwd_k_kernel(BwdParams<T> p) {
+  typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
   constexpr int BKB = 32 * kWaves;
   constexpr int BQ = 32;
-  // tensors: 0 = Q, 1 = dO; statistics: 0 = L log2(e), 1 = D
-  __shared__ __attribute__((aligned(32))) T s_row[2][2][G::kRowElems];
-  __shared__ __attribute__((aligned(32))) T s_tr[2][2][G::kTrElems];
-  __shared__ __attribute__((aligned(16))) float s_stat[2][2][BQ];
+  constexpr int NST = kStages;
+  constexpr int kTile = G::kElems * (int)sizeof(T);
+  // Statistics area: two 256-byte rows (L, D of the tile's 32 queries, then a
+  // copy the upper half-wave writes and nothing reads).
+  constexpr int kStatRow = 64 * (int)sizeof(float);
+  constexpr int kSR = kStatRow / (int)sizeof(float);
+  constexpr int kStage = 2 * kTile + 2 * kStatRow;  // Q, dO, statistics
+  constexpr int kPer = G::kLoads / 2;
+  constexpr int kStatWave = 3;
+  __shared__ __attribute__((aligned(1024))) char s_q[NST * kStage];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, g = lane >> 5;
-  const int nkb = (p.nk + BKB - 1) / BKB;
-  const int lin = xcd_remap(blockIdx.x, nkb * p.batch * p.heads);
-  const int bh = lin / nkb;
-  const int kb = lin % nkb;
+  const int nbh = p.batch * p.heads;
+  const int kb = blockIdx.x / nbh;  // causal: the longest key columns come first
+  const int bh = blockIdx.x - kb * nbh;
   const int b = bh / p.heads, h = bh % p.heads;
   const long rs = (long)p.heads * D;
   const long qbase = ((long)b * p.nq * p.heads + h) * D;
@@ -167,18 +212,17 @@ __global__ void __launch_bounds__(kThreads) bwd_k_kernel(BwdParams<T> p) {
   const int k0 = kb * BKB + wave * 32;
   const int kj = k0 + n;
   const bool kvalid = kj < p.nk;
+  const float scale = p.scale;
 
   const int nqt = (p.nq + BQ - 1) / BQ;
   const int qt_begin = CAUSAL ? (kb * BKB) / BQ : 0;
+  const int total = nqt > qt_begin ? nqt - qt_begin : 0;
 
   f32x16 acc_dk[DT], acc_dv[DT];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    acc_dk[dt] = zero16();
-    acc_dv[dt] = zero16();
-  }
+  for (int dt = 0; dt < DT; ++dt) acc_dk[dt] = acc_dv[dt] = zero16();
 
-  if (qt_begin < nqt) {
+  if (total > 0) {
     V8<T> kf[KS], vf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -186,89 +230,112 @@ __global__ void __launch_bounds__(kThreads) bwd_k_kernel(BwdParams<T> p) {
       kf[ks] = kvalid ? *reinterpret_cast<const V8<T>*>(p.k + off) : zero8<T>();
       vf[ks] = kvalid ? *reinterpret_cast<const V8<T>*>(p.v + off) : zero8<T>();
     }
-    const float scale = p.scale;
     const float c2 = scale * kLog2e;
+    const float inv_scale = 1.0f / scale;
 
-    const T* src = (wave == 0 ? p.q : p.dout) + qbase;
-    TileRegs<T, D> pre;
-    float st_pre = 0.f;
-    // statistics loader: wave 2, lane -> (statistic lane/32, query lane%32)
-    const int st_id = lane >> 5, st_q = lane & 31;
-    const float* st_src = (st_id == 0 ? p.lse : p.delta) + sbase;
-    const float st_mul = st_id == 0 ? kLog2e : 1.f;
-
-    auto load_tile = [&](int qt) {
-      const int q0 = qt * BQ;
-      if (wave < 2) {
-        tile_load<T, D>(pre, src + (long)q0 * rs, rs, p.nq - q0, lane);
-      } else if (wave == 2) {
-        const int qa = q0 + st_q;
-        st_pre = qa < p.nq ? st_src[qa] * st_mul : 0.f;
+    SwzFrags<T, D> fr;
+    fr.init(lane);
+    const int tensor = wave >> 1;  // 0 = Q, 1 = dO
+    const T* src = (tensor == 0 ? p.q : p.dout) + qbase;
+    const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
+    TileDma<T, D, kPer> dma;
+    dma.init(row_bytes, BQ, lane, kPer * (wave & 1));
+    const uint32_t lds0 = lds_base_u32(s_q);
+    auto issue = [&](int i) {
+      const int q0t = (qt_begin + i) * BQ;
+      const uint32_t stage = lds0 + (uint32_t)((i % NST) * kStage);
+      const int nvalid = p.nq - q0t;
+      const T* gsrc = src + (long)q0t * rs;
+      if (nvalid >= BQ) {
+        dma.issue(stage + tensor * kTile, gsrc);
+      } else {
+        TileDma<T, D, kPer> part;
+        part.init(row_bytes, nvalid, lane, kPer * (wave & 1));
+        part.issue(stage + tensor * kTile, gsrc);
+      }
+      if (wave == kStatWave) {
+        // lane l reads query q0t + (l % 32); rows past nq repeat row nq - 1
+        const uint32_t voff = 4u * (uint32_t)min(n, p.nq - 1 - q0t);
+        dma4s(p.lse + sbase + q0t, voff, stage + 2 * kTile);
+        dma4s(p.delta + sbase + q0t, voff, stage + 2 * kTile + kStatRow);
       }
     };
-    auto store_tile = [&](int buf) {
-      if (wave < 2) {
-        tile_store_lds<T, D>(pre, s_row[buf][wave], s_tr[buf][wave], lane);
-      } else if (wave == 2) {
-        s_stat[buf][st_id][st_q] = st_pre;
+    auto finish_stats = [&](int i) {
+      if (wave == kStatWave && g == 0) {
+        float* st = reinterpret_cast<float*>(s_q + (i % NST) * kStage + 2 * kTile);
+        st[n] = -st[n] * inv_scale;
+        st[kSR + n] = -st[kSR + n];
       }
     };
+    // Waits for tile i (the statistics wave issues two more loads per tile).
+    auto wait_for = [&](int i) {
+      if (wave == kStatWave)
+        wait_tile<NST, kPer + 2>(i, total);
+      else
+        wait_tile<NST, kPer>(i, total);
+    };
 
-    load_tile(qt_begin);
-    store_tile(0);
-    __syncthreads();
+    // Retire the key-side loads before the ring starts (see fwd_kernel).
+    wait_vmem();
+#pragma unroll
+    for (int i = 0; i < NST - 1; ++i)
+      if (i < total) issue(i);
 
-    for (int qt = qt_begin; qt < nqt; ++qt) {
-      const int buf = (qt - qt_begin) & 1;
-      const bool has_next = qt + 1 < nqt;
-      if (has_next) load_tile(qt + 1);
-      const int q0 = qt * BQ;
+    for (int i = 0; i < total; ++i) {
+      wait_for(i);
+      finish_stats(i);
+      __syncthreads();
+      if (i + NST - 1 < total) issue(i + NST - 1);
+      const int q0 = (qt_begin + i) * BQ;
       const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0);
       if (active) {
-        const T* sQ = s_row[buf][0];
-        const T* sdO = s_row[buf][1];
-        f32x16 S = zero16(), dP = zero16();
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          S = mma<T>(frag_row<T, D>(sQ, n, g, ks), kf[ks], S);
-          dP = mma<T>(frag_row<T, D>(sdO, n, g, ks), vf[ks], dP);
-        }
-        const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31);
-        f32x16 vP, vdS;
+        const char* st = s_q + (i % NST) * kStage;
+        const float* sc = reinterpret_cast<const float*>(st + 2 * kTile);
+        // S' = S_raw - L / scale, u = dP - D (register r holds query
+        // 8 (r / 4) + 4 g + r % 4 of the tile)
+        f32x16 S, dP;
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
           const int m0 = 8 * a + 4 * g;
-          const f32x4 l2 = *reinterpret_cast<const f32x4*>(&s_stat[buf][0][m0]);
-          const f32x4 dv = *reinterpret_cast<const f32x4*>(&s_stat[buf][1][m0]);
+          const f32x4 v0 = *reinterpret_cast<const f32x4*>(sc + m0);
+          const f32x4 v1 = *reinterpret_cast<const f32x4*>(sc + kSR + m0);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const int r = 4 * a + j;
-            float pv = exp2_fast(S[r] * c2 - l2[j]);
-            if (need_mask) {
-              const int qg = q0 + m0 + j;
-              const bool ok = qg < p.nq && (!CAUSAL || qg >= kj);
-              pv = ok ? pv : 0.f;
-            }
-            vP[r] = pv;
-            vdS[r] = pv * scale * (dP[r] - dv[j]);
+            S[4 * a + j] = v0[j];
+            dP[4 * a + j] = v1[j];
           }
         }
-        const T* tQ = s_tr[buf][0];
-        const T* tdO = s_tr[buf][1];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          S = mma<T>(fr.rowf(st, ks), kf[ks], S);
+          dP = mma<T>(fr.rowf(st + kTile, ks), vf[ks], dP);
+        }
+        f32x16 P;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) P[r] = exp2_fast(S[r] * c2);
+        if ((q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31)) {
+          // visible iff query >= key (causal) and query < nq
+          const int qlo = (CAUSAL ? kj : 0) - q0, qhi = p.nq - q0;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int m = crow(r, g);
+            if (m < qlo || m >= qhi) P[r] = 0.f;
+          }
+        }
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          const V8<T> oP = cvt8<T>(s ? hi8(vP) : lo8(vP));
-          const V8<T> oS = cvt8<T>(s ? hi8(vdS) : lo8(vdS));
+          f32x8 vdS;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vdS[e] = P[8 * s + e] * dP[8 * s + e];  // dS / scale
+          const V8<T> oP = cvt8<T>(s ? hi8(P) : lo8(P));
+          const V8<T> oS = cvt8<T>(vdS);
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
-            const int col = 32 * dt + n;
-            acc_dv[dt] = mma<T>(frag_tr<T, D>(tdO, col, g, s), oP, acc_dv[dt]);
-            acc_dk[dt] = mma<T>(frag_tr<T, D>(tQ, col, g, s), oS, acc_dk[dt]);
+            acc_dv[dt] = mma<T>(fr.trf(st + kTile, dt, s), oP, acc_dv[dt]);
+            acc_dk[dt] = mma<T>(fr.trf(st, dt, s), oS, acc_dk[dt]);
           }
         }
       }
-      if (has_next) store_tile(buf ^ 1);
-      __syncthreads();
     }
   }
 
@@ -283,7 +350,7 @@ __global__ void __launch_bounds__(kThreads) bwd_k_kernel(BwdParams<T> p) {
         f32x4 x, y;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          x[j] = acc_dk[dt][4 * a + j];
+          x[j] = acc_dk[dt][4 * a + j] * scale;
           y[j] = acc_dv[dt][4 * a + j];
         }
         *reinterpret_cast<V4<T>*>(dk + d) = cvt4<T>(x);

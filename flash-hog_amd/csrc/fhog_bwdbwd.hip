@@ -60,23 +60,6 @@ template <typename T, int D> struct Ring {
   static constexpr int value = (sizeof(T) == 2 && D == 64) ? 3 : 2;
 };
 
-// Waits until the tile of iteration `it` (of `total`) has landed in LDS: the
-// loads of at most NST - 2 later tiles may still be in flight.
-template <int NST, int LOADS>
-__device__ __forceinline__ void wait_tile(int it, int total) {
-  if constexpr (NST >= 3) {
-    if (it + NST - 2 < total) {
-      wait_vmem_le<(NST - 2) * LOADS>();
-      return;
-    }
-  }
-  wait_vmem_le<0>();
-}
-
-__device__ __forceinline__ uint32_t lds_base_u32(const void* p) {
-  return __builtin_amdgcn_readfirstlane(lds_addr(p));
-}
-
 // ----------------------------------------------------------------------------
 // Stage 1: passes 1-3, tiled over queries.
 //

@@ -309,6 +309,25 @@ template <int N> __device__ __forceinline__ void wait_vmem_le() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
 }
 
+// Waits until the tile of iteration `it` (of `total`) of an NST-stage ring has
+// landed in LDS, for a wave that issues LOADS loads per tile and keeps NST - 1
+// tiles in flight: the loads of at most NST - 2 later tiles may be outstanding.
+template <int NST, int LOADS>
+__device__ __forceinline__ void wait_tile(int it, int total) {
+  if constexpr (NST >= 3) {
+    if (it + NST - 2 < total) {
+      wait_vmem_le<(NST - 2) * LOADS>();
+      return;
+    }
+  }
+  wait_vmem_le<0>();
+}
+
+// Wave-uniform LDS byte address of p (the M0 operand of the LDS DMAs).
+__device__ __forceinline__ uint32_t lds_base_u32(const void* p) {
+  return __builtin_amdgcn_readfirstlane(lds_addr(p));
+}
+
 // One wave-wide 16-byte-per-lane global -> LDS load addressed as a uniform
 // 64-bit base (SGPR pair) plus a per-lane 32-bit byte offset; lane l's 16 bytes
 // land at lds_byte_addr + 16 l. Untracked by the compiler for the same reason

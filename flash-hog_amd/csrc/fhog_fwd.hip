@@ -5,9 +5,13 @@
 // natural log, of the scaled and masked logits).
 //
 // A workgroup owns 128 queries (4 waves x 32) of one (batch, head) and streams
-// 32-key tiles of K and V through LDS. Scores are computed transposed
-// (S^T = K Q^T) and the output as O^T = V^T P^T, so every lane holds one query
-// row in both: the online-softmax rescale is a per-lane scalar multiply.
+// 32-key tiles of K and V global -> LDS (no registers) through a 3-stage ring
+// of XOR-swizzled tiles, one barrier per tile; wave w loads half (w % 2) of
+// tensor w / 2. Scores are computed transposed (S^T = K Q^T) and the output
+// as O^T = V^T P^T, so every lane holds one query row in both: the online-
+// softmax rescale is a per-lane scalar multiply, skipped when no row of the
+// wave raised its running maximum. Causal blocks are issued longest first with
+// (batch, head) as the minor index (see fhog_bwdbwd.hip).
 #include "fhog_device.h"
 #include "fhog_params.h"
 
@@ -17,23 +21,37 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kStages = 3;
+
+// Waves per SIMD the register allocator is asked to allow: two for 2-byte
+// types at D = 64, one otherwise.
+template <typename T, int D> struct Occupancy {
+  static constexpr int value = (sizeof(T) == 2 && D == 64) ? 2 : 1;
+};
 
 template <typename T, int D, bool CAUSAL>
-__global__ void __launch_bounds__(kThreads) fwd_kernel(FwdParams<T> p) {
-  typedef TileGeom<T, D> G;
+__global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
+fwd_kernel(FwdParams<T> p) {
+  typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
   constexpr int BQ = 32 * kWaves;
   constexpr int BK = 32;
-  __shared__ __attribute__((aligned(32))) T s_row[2][2][G::kRowElems];  // K, V
-  __shared__ __attribute__((aligned(32))) T s_tr[2][2][G::kTrElems];
+  constexpr int NST = kStages;
+  constexpr int kTile = G::kElems * (int)sizeof(T);
+  constexpr int kStage = 2 * kTile;  // K, V
+  constexpr int kPer = G::kLoads / 2;
+  __shared__ __attribute__((aligned(1024))) char s_kv[NST * kStage];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, g = lane >> 5;
   const int nqb = (p.nq + BQ - 1) / BQ;
-  const int lin = xcd_remap(blockIdx.x, nqb * p.batch * p.heads);
-  const int bh = lin / nqb;
-  const int qb = CAUSAL ? nqb - 1 - lin % nqb : lin % nqb;
+  const int nbh = p.batch * p.heads;
+  const int rank = blockIdx.x / nbh;
+  const int bh = blockIdx.x - rank * nbh;
+  const int qb = CAUSAL ? nqb - 1 - rank : rank;
   const int b = bh / p.heads, h = bh % p.heads;
   const long rs = (long)p.heads * D;
   const long qbase = ((long)b * p.nq * p.heads + h) * D;
@@ -57,6 +75,27 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(FwdParams<T> p) {
   if (CAUSAL) wend = min(wend, q0 + 32);
   const int wkt = q0 < p.nq ? (wend + BK - 1) / BK : 0;
 
+  SwzFrags<T, D> fr;
+  fr.init(lane);
+  const int tensor = wave >> 1;  // 0 = K, 1 = V
+  const T* src = (tensor == 0 ? p.k : p.v) + kbase;
+  const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
+  TileDma<T, D, kPer> dma;
+  dma.init(row_bytes, BK, lane, kPer * (wave & 1));
+  const uint32_t lds_tensor = lds_base_u32(s_kv) + tensor * kTile;
+  auto issue = [&](int kt) {
+    const int nvalid = p.nk - kt * BK;
+    const uint32_t dst = lds_tensor + (uint32_t)((kt % NST) * kStage);
+    const T* gsrc = src + (long)kt * BK * rs;
+    if (nvalid >= BK) {
+      dma.issue(dst, gsrc);
+    } else {
+      TileDma<T, D, kPer> part;
+      part.init(row_bytes, nvalid, lane, kPer * (wave & 1));
+      part.issue(dst, gsrc);
+    }
+  };
+
   const float c2 = p.scale * kLog2e;
   float m = -1e30f;  // running row max of the log2-domain logits
   float lpart = 0.f; // this lane's share of the running row sum
@@ -64,61 +103,57 @@ __global__ void __launch_bounds__(kThreads) fwd_kernel(FwdParams<T> p) {
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = zero16();
 
-  const bool loader = wave < 2;
-  const T* src = (wave == 0 ? p.k : p.v) + kbase;
-  TileRegs<T, D> pre;
-  if (loader) {
-    tile_load<T, D>(pre, src, rs, p.nk, lane);
-    tile_store_lds<T, D>(pre, s_row[0][wave], s_tr[0][wave], lane);
-  }
-  __syncthreads();
+  // Retire the query loads before the ring starts: otherwise the compiler waits
+  // for them at their first use inside the loop, and that wait (vmcnt counts
+  // the untracked LDS DMAs too) would drain the prefetched tiles.
+  wait_vmem();
+#pragma unroll
+  for (int i = 0; i < NST - 1; ++i)
+    if (i < nkt) issue(i);
 
   for (int kt = 0; kt < nkt; ++kt) {
-    const int buf = kt & 1;
-    const bool has_next = kt + 1 < nkt;
-    if (has_next && loader) tile_load<T, D>(pre, src + (long)(kt + 1) * BK * rs, rs, p.nk - (kt + 1) * BK, lane);
+    wait_tile<NST, kPer>(kt, nkt);
+    __syncthreads();
+    if (kt + NST - 1 < nkt) issue(kt + NST - 1);
     if (kt < wkt) {
-      const T* sK = s_row[buf][0];
+      const char* st = s_kv + (kt % NST) * kStage;
       f32x16 S = zero16();
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) S = mma<T>(frag_row<T, D>(sK, n, g, ks), qf[ks], S);
-      const int k0 = kt * BK;
-      const bool need_mask = (k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0);
-      float mloc = -1e30f;
+      for (int ks = 0; ks < KS; ++ks) S = mma<T>(fr.rowf(st, ks), qf[ks], S);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float s2 = S[r] * c2;
-        if (need_mask) {
-          const int kj = k0 + crow(r, g);
-          const bool ok = kj < p.nk && (!CAUSAL || kj <= qi);
-          s2 = ok ? s2 : -INFINITY;
-        }
-        S[r] = s2;
-        mloc = fmaxf(mloc, s2);
+      for (int r = 0; r < 16; ++r) S[r] *= c2;
+      const int k0 = kt * BK;
+      if ((k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0)) {
+        const int klim = min(p.nk - 1, CAUSAL ? qi : p.nk - 1) - k0;  // last visible key, tile-relative
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (crow(r, g) > klim) S[r] = -INFINITY;
       }
+      float mloc = S[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, S[r]);
       const float mnew = fmaxf(m, xgroup_max(mloc));
-      const float alpha = exp2_fast(m - mnew);
-      m = mnew;
+      if (__any(mnew != m)) {
+        const float alpha = exp2_fast(m - mnew);
+        lpart *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
+        m = mnew;
+      }
       float psum = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = exp2_fast(S[r] - mnew);  // masked: exp2(-inf) = 0
-        S[r] = pv;
-        psum += pv;
+        S[r] = exp2_fast(S[r] - m);  // masked: exp2(-inf) = 0
+        psum += S[r];
       }
-      lpart = lpart * alpha + psum;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
-      const T* tV = s_tr[buf][1];
+      lpart += psum;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const V8<T> oP = cvt8<T>(s ? hi8(S) : lo8(S));
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] = mma<T>(frag_tr<T, D>(tV, 32 * dt + n, g, s), oP, acc[dt]);
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = mma<T>(fr.trf(st + kTile, dt, s), oP, acc[dt]);
       }
     }
-    if (has_next && loader) tile_store_lds<T, D>(pre, s_row[buf ^ 1][wave], s_tr[buf ^ 1][wave], lane);
-    __syncthreads();
   }
 
   const float l = xgroup_sum(lpart);
