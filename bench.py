@@ -15,6 +15,16 @@ algorithmic share is the 9 products it is first to need (18 * d per pair),
 timed per launch with HIP events on the stream it runs on.
 
 Prints one JSON line on stdout; progress goes to stderr.
+
+    python bench.py --hvp-table {b1,tokens}
+
+times instead the end-to-end causal-attention Hessian-vector product through
+the public front-end (forward + first backward + double backward), on the
+shapes of the reference's HVP tables (flash_hog/csrc/tk_bwdbwd/BENCHMARKS.md:
+12 heads, head_dim 64, causal, fp32 inputs cast to bf16 around the attention
+call; "b1" = batch 1 at sequence 512 ... 131072, "tokens" = batch x sequence
+= 262144). Prints one markdown row per shape on stderr and one JSON line per
+shape on stdout.
 """
 
 from __future__ import annotations
@@ -111,6 +121,94 @@ def cpu_baseline(args, B, N, H, D, scale, causal):
     }
 
 
+HVP_TABLES = {
+    "b1": [(1, 512 << i) for i in range(9)],
+    "tokens": [(262144 // (512 << i), 512 << i) for i in range(9)],
+}
+
+
+def hvp_table(args):
+    """Mean HVP time per shape (the reference's protocol: warm-up, then 10
+    iterations, 5 at sequence >= 16k, 3 at >= 64k) and faithfulness: cosine
+    similarity and max relative error of the concatenated (q, k, v) HVP against
+    a dense fp32 torch-autograd HVP of the same function where that fits
+    (batch * sequence^2 <= 2048^2), else against the same HVP through this
+    library's fp32 kernels (sequence <= 16384), else not measured."""
+    import torch
+
+    import flash_hog
+
+    dev = torch.device("cuda:0")
+    H, D = 12, 64
+    scale = D ** -0.5
+
+    def attn_flash(dtype):
+        def f(q, k, v):
+            return flash_hog.dot_product_attention(q.to(dtype), k.to(dtype), v.to(dtype), is_causal=True,
+                                                   scale=scale).float()
+        return f
+
+    def attn_dense(q, k, v):
+        qh, kh, vh = (t.permute(0, 2, 1, 3).contiguous() for t in (q, k, v))
+        s = torch.matmul(qh, kh.transpose(-1, -2).contiguous()) * scale
+        n = s.shape[-1]
+        s = s.masked_fill(torch.ones(n, n, device=s.device, dtype=torch.bool).triu(1), float("-inf"))
+        return torch.matmul(torch.softmax(s, dim=-1), vh).permute(0, 2, 1, 3)
+
+    def hvp(attn, x, cot, tan):
+        """grad of <grad(loss), tan> with loss = <attn(x), cot>, as the reference's make_hvp."""
+        x = [t.detach().requires_grad_(True) for t in x]
+        loss = (attn(*x) * cot).sum()
+        g = torch.autograd.grad(loss, x, create_graph=True)
+        return torch.autograd.grad(g, x, tan)
+
+    def compare(a, r):
+        a = torch.cat([t.double().flatten() for t in a])
+        r = torch.cat([t.double().flatten() for t in r])
+        cos = float(torch.dot(a, r) / (a.norm() * r.norm()))
+        return cos, float((a - r).abs().max() / r.abs().max())
+
+    rows = []
+    log("| batch | seq | HVP (ms) | faithfulness |")
+    log("|--:|--:|--:|:--|")
+    for B, N in HVP_TABLES[args.hvp_table]:
+        gen = torch.Generator().manual_seed(B * 7919 + N)
+        mk = lambda: torch.randn((B, N, H, D), generator=gen).to(dev)
+        x, cot, tan = [mk(), mk(), mk()], mk(), [mk(), mk(), mk()]
+        f = attn_flash(torch.bfloat16)
+        iters = 3 if N >= 65536 else 5 if N >= 16384 else 10
+        for _ in range(2):
+            out = hvp(f, x, cot, tan)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            out = hvp(f, x, cot, tan)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / iters
+        if B * N * N <= 2048 * 2048:
+            ref, against = hvp(attn_dense, x, cot, tan), "dense fp32"
+        elif N <= 16384:
+            ref, against = hvp(attn_flash(torch.float32), x, cot, tan), "fp32 kernels"
+        else:
+            ref, against = None, None
+        faith = "not measured"
+        row = {"table": args.hvp_table, "batch": B, "seq": N, "heads": H, "head_dim": D, "hvp_ms": round(ms, 4),
+               "iterations": iters}
+        if ref is not None:
+            cos, rel = compare(out, ref)
+            faith = f"cos {cos:.4f}, max rel err {rel:.1e} vs {against}"
+            row.update(cos=round(cos, 6), max_rel_err=rel, against=against)
+        torch.cuda.synchronize()
+        log(f"| {B} | {N} | {ms:.2f} | {faith} |")
+        print(json.dumps(row), flush=True)
+        rows.append(row)
+        del x, cot, tan, out, ref
+        torch.cuda.empty_cache()
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description="Flash-HOG double-backward benchmark")
     ap.add_argument("--gpus", type=int, default=1)
@@ -121,6 +219,8 @@ def main(argv=None):
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (PMC byte-counter calibration)")
+    ap.add_argument("--hvp-table", choices=sorted(HVP_TABLES),
+                    help="time the end-to-end HVP on the shapes of one of the reference's HVP tables instead")
     args = ap.parse_args(argv)
 
     if args.gpus != 1:
@@ -128,6 +228,8 @@ def main(argv=None):
               f"(batch, head) with no exchange, so whole-job throughput at N GPUs is N x the one-GPU value.",
               file=sys.stderr)
         return 2
+    if args.hvp_table:
+        return hvp_table(args)
 
     import torch
 

@@ -33,13 +33,18 @@ bool aligned(const void* p, uintptr_t bytes) {
 }
 
 struct Shape {
-  int batch, n_q, n_k, heads, kv_heads, head_dim, dtype;
+  int batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal;
   float scale;
+  // Key j is visible to query i iff j <= i + coff (causal kernels only).
+  int coff() const { return causal == FHOG_CAUSAL_BOTTOM_RIGHT ? n_k - n_q : 0; }
 };
 
 int check_shape(const Shape& s, const char* who) {
   if (!(s.scale == s.scale) || s.scale - s.scale != 0.0f)
     return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: scale must be finite", who);
+  if (s.causal != FHOG_CAUSAL_NONE && s.causal != FHOG_CAUSAL_TOP_LEFT && s.causal != FHOG_CAUSAL_BOTTOM_RIGHT)
+    return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: causal must be 0 (none), 1 (top-left) or 2 (bottom-right), got %d",
+                who, s.causal);
   if (s.batch < 1 || s.n_q < 1 || s.n_k < 1 || s.heads < 1 || s.kv_heads < 1)
     return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: sizes must be >= 1 (batch=%d n_q=%d n_k=%d heads=%d kv_heads=%d)",
                 who, s.batch, s.n_q, s.n_k, s.heads, s.kv_heads);
@@ -50,9 +55,6 @@ int check_shape(const Shape& s, const char* who) {
   if (s.heads % s.kv_heads != 0)
     return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: heads (%d) must be a multiple of kv_heads (%d)", who, s.heads,
                 s.kv_heads);
-  if (s.heads != s.kv_heads)
-    return fail(FHOG_ERR_UNSUPPORTED, "%s: grouped-query attention (heads=%d, kv_heads=%d) is not supported", who,
-                s.heads, s.kv_heads);
   if (s.head_dim != 64 && s.head_dim != 128)
     return fail(FHOG_ERR_UNSUPPORTED, "%s: head_dim must be 64 or 128, got %d", who, s.head_dim);
   if (s.dtype == FHOG_DTYPE_F32 && s.head_dim != 64)
@@ -100,7 +102,7 @@ hipError_t dispatch(int dtype, int head_dim, bool causal, F&& f) {
 
 extern "C" {
 
-int fhog_abi_version(void) { return 100; }
+int fhog_abi_version(void) { return 101; }
 
 const char* fhog_status_string(int status) {
   switch (status) {
@@ -123,11 +125,12 @@ int fhog_attention_fwd(fhog_stream_t stream, const void* q, const void* k, const
                        int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim, int dtype, int causal,
                        float scale) {
   static const char* who = "fhog_attention_fwd";
-  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, scale};
+  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal, scale};
   if (int st = check_shape(s, who)) return st;
   if (int st = check_ptrs(who, {{"q", q}, {"k", k}, {"v", v}, {"o", o}}, {{"lse", lse}})) return st;
   auto run = [&]<typename T, int D, bool C>() {
-    fhog::FwdParams<T> p{(const T*)q, (const T*)k, (const T*)v, (T*)o, lse, batch, n_q, n_k, heads, scale};
+    fhog::FwdParams<T> p{(const T*)q, (const T*)k, (const T*)v, (T*)o, lse, batch, n_q, n_k, heads, kv_heads,
+                         s.coff(), scale};
     return fhog::launch_fwd<T, D, C>(p, (hipStream_t)stream);
   };
   return launch_status(dispatch(dtype, head_dim, causal != 0, run), who);
@@ -137,7 +140,7 @@ int fhog_attention_bwd(fhog_stream_t stream, const void* q, const void* k, const
                        const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta, int batch,
                        int n_q, int n_k, int heads, int kv_heads, int head_dim, int dtype, int causal, float scale) {
   static const char* who = "fhog_attention_bwd";
-  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, scale};
+  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal, scale};
   if (int st = check_shape(s, who)) return st;
   if (int st = check_ptrs(who, {{"q", q}, {"k", k}, {"v", v}, {"o", o}, {"dout", dout}, {"dq", dq}, {"dk", dk},
                                 {"dv", dv}},
@@ -145,7 +148,7 @@ int fhog_attention_bwd(fhog_stream_t stream, const void* q, const void* k, const
     return st;
   auto run = [&]<typename T, int D, bool C>() {
     fhog::BwdParams<T> p{(const T*)q, (const T*)k, (const T*)v, (const T*)o, (const T*)dout, lse,
-                         (T*)dq, (T*)dk, (T*)dv, delta, batch, n_q, n_k, heads, scale};
+                         (T*)dq, (T*)dk, (T*)dv, delta, batch, n_q, n_k, heads, kv_heads, s.coff(), scale};
     return fhog::launch_bwd<T, D, C>(p, (hipStream_t)stream);
   };
   return launch_status(dispatch(dtype, head_dim, causal != 0, run), who);
@@ -158,7 +161,7 @@ int bwdbwd_impl(const char* who, int stages, fhog_stream_t stream, const void* q
                 const float* lse, void* dq2, void* dk2, void* dv2, void* ddo, float* delta, float* ddelta,
                 float* bstat, int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim, int dtype,
                 int causal, float scale) {
-  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, scale};
+  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal, scale};
   if (int st = check_shape(s, who)) return st;
   if (int st = check_ptrs(who, {{"q", q}, {"k", k}, {"v", v}, {"dout", dout}, {"ddq", ddq}, {"ddk", ddk},
                                 {"ddv", ddv}},
@@ -173,7 +176,7 @@ int bwdbwd_impl(const char* who, int stages, fhog_stream_t stream, const void* q
                             (const T*)ddq, (const T*)ddk, (const T*)ddv, lse,         (T*)dq2,
                             (T*)dk2,       (T*)dv2,       (T*)ddo,       delta,       ddelta,
                             bstat,         batch,         n_q,           n_k,         heads,
-                            scale};
+                            kv_heads,      s.coff(),      scale};
     return fhog::launch_bwdbwd<T, D, C>(p, (hipStream_t)stream, stages);
   };
   return launch_status(dispatch(dtype, head_dim, causal != 0, run), who);

@@ -57,9 +57,11 @@ bwd_q_kernel(BwdParams<T> p) {
   const int bh = blockIdx.x - rank * nbh;
   const int qb = CAUSAL ? nqb - 1 - rank : rank;
   const int b = bh / p.heads, h = bh % p.heads;
-  const long rs = (long)p.heads * D;
+  const int hk = h / (p.heads / p.kv_heads);
+  const long rs = (long)p.heads * D;      // query-side row stride
+  const long rsk = (long)p.kv_heads * D;  // key-side row stride
   const long qbase = ((long)b * p.nq * p.heads + h) * D;
-  const long kbase = ((long)b * p.nk * p.heads + h) * D;
+  const long kbase = ((long)b * p.nk * p.kv_heads + hk) * D;
   const long sbase = (long)bh * p.nq;
   const int q0 = qb * BQ + wave * 32;
   const int qi = q0 + n;
@@ -85,10 +87,10 @@ bwd_q_kernel(BwdParams<T> p) {
   const float nL2 = qvalid ? -p.lse[sbase + qi] * kLog2e : 0.f;
 
   int kend = p.nk;
-  if (CAUSAL) kend = min(kend, qb * BQ + BQ);
+  if (CAUSAL) kend = max(0, min(kend, qb * BQ + BQ + p.coff));
   const int nkt = (kend + BK - 1) / BK;
   int wend = p.nk;
-  if (CAUSAL) wend = min(wend, q0 + 32);
+  if (CAUSAL) wend = max(0, min(wend, q0 + 32 + p.coff));
   const int wkt = q0 < p.nq ? (wend + BK - 1) / BK : 0;
 
   const float scale = p.scale;
@@ -101,14 +103,14 @@ bwd_q_kernel(BwdParams<T> p) {
   fr.init(lane);
   const int tensor = wave >> 1;  // 0 = K, 1 = V
   const T* src = (tensor == 0 ? p.k : p.v) + kbase;
-  const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
+  const uint32_t row_bytes = (uint32_t)(rsk * (long)sizeof(T));
   TileDma<T, D, kPer> dma;
   dma.init(row_bytes, BK, lane, kPer * (wave & 1));
   const uint32_t lds_tensor = lds_base_u32(s_kv) + tensor * kTile;
   auto issue = [&](int kt) {
     const int nvalid = p.nk - kt * BK;
     const uint32_t dst = lds_tensor + (uint32_t)((kt % NST) * kStage);
-    const T* gsrc = src + (long)kt * BK * rs;
+    const T* gsrc = src + (long)kt * BK * rsk;
     if (nvalid >= BK) {
       dma.issue(dst, gsrc);
     } else {
@@ -140,8 +142,8 @@ bwd_q_kernel(BwdParams<T> p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) P[r] = exp2_fast(fmaf(S[r], c2, nL2));
       const int k0 = kt * BK;
-      if ((k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0)) {
-        const int klim = min(p.nk - 1, CAUSAL ? qi : p.nk - 1) - k0;  // last visible key, tile-relative
+      if ((k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0 + p.coff)) {
+        const int klim = min(p.nk - 1, CAUSAL ? qi + p.coff : p.nk - 1) - k0;  // last visible key, tile-relative
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           if (crow(r, g) > klim) P[r] = 0.f;
@@ -201,22 +203,27 @@ bwd_k_kernel(BwdParams<T> p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, g = lane >> 5;
-  const int nbh = p.batch * p.heads;
+  const int nbh = p.batch * p.kv_heads;
   const int kb = blockIdx.x / nbh;  // causal: the longest key columns come first
   const int bh = blockIdx.x - kb * nbh;
-  const int b = bh / p.heads, h = bh % p.heads;
-  const long rs = (long)p.heads * D;
-  const long qbase = ((long)b * p.nq * p.heads + h) * D;
-  const long kbase = ((long)b * p.nk * p.heads + h) * D;
-  const long sbase = (long)bh * p.nq;
+  const int b = bh / p.kv_heads, hk = bh % p.kv_heads;
+  const int grp = p.heads / p.kv_heads;  // query heads per key/value head
+  const long rs = (long)p.heads * D;      // query-side row stride
+  const long rsk = (long)p.kv_heads * D;  // key-side row stride
+  // query head hk * grp + gi: tensors at qbase + gi * D, statistics at sbase + gi * nq
+  const long qbase = ((long)b * p.nq * p.heads + (long)hk * grp) * D;
+  const long kbase = ((long)b * p.nk * p.kv_heads + hk) * D;
+  const long sbase = ((long)b * p.heads + (long)hk * grp) * p.nq;
   const int k0 = kb * BKB + wave * 32;
   const int kj = k0 + n;
   const bool kvalid = kj < p.nk;
   const float scale = p.scale;
 
+  // Iteration i visits query tile qt_begin + i / grp of query head
+  // hk * grp + i % grp: the heads of a group share each tile's causal bounds.
   const int nqt = (p.nq + BQ - 1) / BQ;
-  const int qt_begin = CAUSAL ? (kb * BKB) / BQ : 0;
-  const int total = nqt > qt_begin ? nqt - qt_begin : 0;
+  const int qt_begin = CAUSAL ? max(0, kb * BKB - p.coff) / BQ : 0;
+  const int total = nqt > qt_begin ? (nqt - qt_begin) * grp : 0;
 
   f32x16 acc_dk[DT], acc_dv[DT];
 #pragma unroll
@@ -226,7 +233,7 @@ bwd_k_kernel(BwdParams<T> p) {
     V8<T> kf[KS], vf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const long off = kbase + (long)kj * rs + 16 * ks + 8 * g;
+      const long off = kbase + (long)kj * rsk + 16 * ks + 8 * g;
       kf[ks] = kvalid ? *reinterpret_cast<const V8<T>*>(p.k + off) : zero8<T>();
       vf[ks] = kvalid ? *reinterpret_cast<const V8<T>*>(p.v + off) : zero8<T>();
     }
@@ -242,10 +249,12 @@ bwd_k_kernel(BwdParams<T> p) {
     dma.init(row_bytes, BQ, lane, kPer * (wave & 1));
     const uint32_t lds0 = lds_base_u32(s_q);
     auto issue = [&](int i) {
-      const int q0t = (qt_begin + i) * BQ;
+      const int qt = i / grp, gi = i - qt * grp;
+      const int q0t = (qt_begin + qt) * BQ;
       const uint32_t stage = lds0 + (uint32_t)((i % NST) * kStage);
       const int nvalid = p.nq - q0t;
-      const T* gsrc = src + (long)q0t * rs;
+      const T* gsrc = src + (long)gi * D + (long)q0t * rs;
+      const long sb = sbase + (long)gi * p.nq;
       if (nvalid >= BQ) {
         dma.issue(stage + tensor * kTile, gsrc);
       } else {
@@ -256,8 +265,8 @@ bwd_k_kernel(BwdParams<T> p) {
       if (wave == kStatWave) {
         // lane l reads query q0t + (l % 32); rows past nq repeat row nq - 1
         const uint32_t voff = 4u * (uint32_t)min(n, p.nq - 1 - q0t);
-        dma4s(p.lse + sbase + q0t, voff, stage + 2 * kTile);
-        dma4s(p.delta + sbase + q0t, voff, stage + 2 * kTile + kStatRow);
+        dma4s(p.lse + sb + q0t, voff, stage + 2 * kTile);
+        dma4s(p.delta + sb + q0t, voff, stage + 2 * kTile + kStatRow);
       }
     };
     auto finish_stats = [&](int i) {
@@ -286,8 +295,8 @@ bwd_k_kernel(BwdParams<T> p) {
       finish_stats(i);
       __syncthreads();
       if (i + NST - 1 < total) issue(i + NST - 1);
-      const int q0 = (qt_begin + i) * BQ;
-      const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0);
+      const int q0 = (qt_begin + i / grp) * BQ;
+      const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
       if (active) {
         const char* st = s_q + (i % NST) * kStage;
         const float* sc = reinterpret_cast<const float*>(st + 2 * kTile);
@@ -313,9 +322,9 @@ bwd_k_kernel(BwdParams<T> p) {
         f32x16 P;
 #pragma unroll
         for (int r = 0; r < 16; ++r) P[r] = exp2_fast(S[r] * c2);
-        if ((q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31)) {
-          // visible iff query >= key (causal) and query < nq
-          const int qlo = (CAUSAL ? kj : 0) - q0, qhi = p.nq - q0;
+        if ((q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31 - p.coff)) {
+          // visible iff query >= key - coff (causal) and query < nq
+          const int qlo = (CAUSAL ? kj - p.coff : 0) - q0, qhi = p.nq - q0;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int m = crow(r, g);
@@ -340,8 +349,8 @@ bwd_k_kernel(BwdParams<T> p) {
   }
 
   if (kvalid) {
-    T* dk = p.dk + kbase + (long)kj * rs;
-    T* dv = p.dv + kbase + (long)kj * rs;
+    T* dk = p.dk + kbase + (long)kj * rsk;
+    T* dv = p.dv + kbase + (long)kj * rsk;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
@@ -364,13 +373,12 @@ bwd_k_kernel(BwdParams<T> p) {
 
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t stream) {
-  const int nbh = p.batch * p.heads;
   const int nqb = (p.nq + 32 * kWaves - 1) / (32 * kWaves);
   const int nkb = (p.nk + 32 * kWaves - 1) / (32 * kWaves);
-  hipLaunchKernelGGL((bwd_q_kernel<T, D, CAUSAL>), dim3(nqb * nbh), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((bwd_q_kernel<T, D, CAUSAL>), dim3(nqb * p.batch * p.heads), dim3(kThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL>), dim3(nkb * nbh), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL>), dim3(nkb * p.batch * p.kv_heads), dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
 

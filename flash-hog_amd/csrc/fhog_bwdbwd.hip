@@ -94,9 +94,11 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   const int bh = blockIdx.x - rank * nbh;
   const int qb = CAUSAL ? nqb - 1 - rank : rank;
   const int b = bh / p.heads, h = bh % p.heads;
-  const long rs = (long)p.heads * D;
+  const int hk = h / (p.heads / p.kv_heads);
+  const long rs = (long)p.heads * D;      // query-side row stride
+  const long rsk = (long)p.kv_heads * D;  // key-side row stride
   const long qbase = ((long)b * p.nq * p.heads + h) * D;
-  const long kbase = ((long)b * p.nk * p.heads + h) * D;
+  const long kbase = ((long)b * p.nk * p.kv_heads + hk) * D;
   const long sbase = (long)bh * p.nq;
   const int q0 = qb * BQ + wave * 32;
   const int qi = q0 + n;
@@ -127,10 +129,10 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   const float nL2 = qvalid ? -p.lse[sbase + qi] * kLog2e : 0.f;
 
   int kend = p.nk;
-  if (CAUSAL) kend = min(kend, qb * BQ + BQ);
+  if (CAUSAL) kend = max(0, min(kend, qb * BQ + BQ + p.coff));
   const int nkt = (kend + BK - 1) / BK;                   // tiles the workgroup streams
   int wend = p.nk;
-  if (CAUSAL) wend = min(wend, q0 + 32);
+  if (CAUSAL) wend = max(0, min(wend, q0 + 32 + p.coff));
   const int wkt = q0 < p.nq ? (wend + BK - 1) / BK : 0;  // tiles with work for this wave
 
   SwzFrags<T, D> fr;
@@ -139,7 +141,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   // Wave w streams tensor w; the key sequence is streamed twice (iterations
   // 0 .. nkt-1 and nkt .. 2 nkt - 1).
   const T* src = (wave == 0 ? p.k : wave == 1 ? p.v : wave == 2 ? p.ddk : p.ddv) + kbase;
-  const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
+  const uint32_t row_bytes = (uint32_t)(rsk * (long)sizeof(T));
   TileDma<T, D> dma;
   dma.init(row_bytes, BK, lane);
   const uint32_t lds_wave = lds_base_u32(s_kv) + wave * kTile;
@@ -153,7 +155,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
     const int kt = it < nkt ? it : it - nkt;
     const int nvalid = p.nk - kt * BK;
     const uint32_t dst = lds_wave + (uint32_t)((it % NST) * kStage);
-    const T* gsrc = src + (long)kt * BK * rs;
+    const T* gsrc = src + (long)kt * BK * rsk;
     if (nvalid >= BK) {
       dma.issue(dst, gsrc);
     } else {
@@ -176,9 +178,9 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   // Masks P on a diagonal or ragged tile (uniform branch).
   auto mask_probs = [&](f32x16& P, int kt) {
     const int k0 = kt * BK;
-    const bool need_mask = (k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0);
+    const bool need_mask = (k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0 + p.coff);
     if (need_mask) {
-      const int klim = min(p.nk - 1, CAUSAL ? qi : p.nk - 1) - k0;  // last visible key, tile-relative
+      const int klim = min(p.nk - 1, CAUSAL ? qi + p.coff : p.nk - 1) - k0;  // last visible key, tile-relative
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (crow(r, g) > klim) P[r] = 0.f;
@@ -351,20 +353,26 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, g = lane >> 5;
-  const int nbh = p.batch * p.heads;
+  const int nbh = p.batch * p.kv_heads;
   const int kb = blockIdx.x / nbh;  // causal: the longest key columns come first
   const int bh = blockIdx.x - kb * nbh;
-  const int b = bh / p.heads, h = bh % p.heads;
-  const long rs = (long)p.heads * D;
-  const long qbase = ((long)b * p.nq * p.heads + h) * D;
-  const long kbase = ((long)b * p.nk * p.heads + h) * D;
-  const long sbase = (long)bh * p.nq;
+  const int b = bh / p.kv_heads, hk = bh % p.kv_heads;
+  const int grp = p.heads / p.kv_heads;  // query heads per key/value head
+  const long rs = (long)p.heads * D;      // query-side row stride
+  const long rsk = (long)p.kv_heads * D;  // key-side row stride
+  // query head hk * grp + gi: tensors at qbase + gi * D, statistics at sbase + gi * nq
+  const long qbase = ((long)b * p.nq * p.heads + (long)hk * grp) * D;
+  const long kbase = ((long)b * p.nk * p.kv_heads + hk) * D;
+  const long sbase = ((long)b * p.heads + (long)hk * grp) * p.nq;
   const int k0 = kb * BKB + wave * 32;
   const int kj = k0 + n;
   const bool kvalid = kj < p.nk;
 
+  // Iteration i visits query tile qt_begin + i / grp of query head
+  // hk * grp + i % grp (the group reduction of
+  // flash_hog/jax/_pallas_gpu_kernel.py:333-370, in one ring).
   const int nqt = (p.nq + BQ - 1) / BQ;
-  const int qt_begin = CAUSAL ? (kb * BKB) / BQ : 0;
+  const int qt_begin = CAUSAL ? max(0, kb * BKB - p.coff) / BQ : 0;
 
   f32x16 acc_dk2[DT], acc_dv2[DT];
 #pragma unroll
@@ -378,7 +386,7 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
     V8<T> kf[KS], dkf[KS], vf[KS], dvf[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const long off = kbase + (long)kj * rs + 16 * ks + 8 * g;
+      const long off = kbase + (long)kj * rsk + 16 * ks + 8 * g;
       if (kvalid) {
         kf[ks] = *reinterpret_cast<const V8<T>*>(p.k + off);
         dkf[ks] = *reinterpret_cast<const V8<T>*>(p.ddk + off);
@@ -397,7 +405,7 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
     SwzFrags<T, D> fr;
     fr.init(lane);
 
-    const int total = nqt - qt_begin;
+    const int total = (nqt - qt_begin) * grp;
     // Retire the key-side loads before the ring starts (see bwdbwd_q_kernel).
     wait_vmem();
     const T* src = (wave == 0 ? p.q : wave == 1 ? p.dout : p.ddq) + qbase;
@@ -413,10 +421,12 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
     // -L / scale, -dD / scale, -D, -(D dD + B).
     constexpr int kStatLoads = 2;
     auto issue_stats = [&](int i) {
-      const int q = min((qt_begin + i) * BQ + n, p.nq - 1);
+      const int qt = i / grp, gi = i - qt * grp;
+      const int q = min((qt_begin + qt) * BQ + n, p.nq - 1);
+      const long sb = sbase + (long)gi * p.nq;
       const uint32_t dst = lds_base_u32(s_q) + (uint32_t)((i % NST) * kStage + 3 * kTile);
-      dma4((g ? p.delta : p.lse) + sbase + q, dst);
-      dma4((g ? p.bstat : p.ddelta) + sbase + q, dst + 256);
+      dma4((g ? p.delta : p.lse) + sb + q, dst);
+      dma4((g ? p.bstat : p.ddelta) + sb + q, dst + 256);
     };
     const float inv_scale = 1.0f / scale;
     auto finish_stats = [&](int i) {
@@ -445,10 +455,11 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
         issue_stats(i);
         return;
       }
-      const int q0t = (qt_begin + i) * BQ;
+      const int qt = i / grp, gi = i - qt * grp;
+      const int q0t = (qt_begin + qt) * BQ;
       const int nvalid = p.nq - q0t;
       const uint32_t dst = lds_wave + (uint32_t)((i % NST) * kStage);
-      const T* gsrc = src + (long)q0t * rs;
+      const T* gsrc = src + (long)gi * D + (long)q0t * rs;
       if (nvalid >= BQ) {
         dma.issue(dst, gsrc);
       } else {
@@ -469,9 +480,8 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
       if (wave < 3) wait_tile<NST, G::kLoads>(i, total);
       __syncthreads();
       if (i + NST - 1 < total) issue(i + NST - 1);
-      const int qt = qt_begin + i;
-      const int q0 = qt * BQ;
-      const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0);
+      const int q0 = (qt_begin + i / grp) * BQ;
+      const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
       if (active) {
         const char* st = s_q + (i % NST) * kStage;
         const char* sQ = st;
@@ -512,10 +522,10 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
         f32x16 P;
 #pragma unroll
         for (int r = 0; r < 16; ++r) P[r] = exp2_fast(S[r] * c2);
-        const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31);
+        const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31 - p.coff);
         if (need_mask) {
-          // visible iff query >= key (causal) and query < nq
-          const int qlo = (CAUSAL ? kj : 0) - q0, qhi = p.nq - q0;
+          // visible iff query >= key - coff (causal) and query < nq
+          const int qlo = (CAUSAL ? kj - p.coff : 0) - q0, qhi = p.nq - q0;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int m = crow(r, g);
@@ -555,8 +565,8 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
 
   if (kvalid) {
     const float scale = p.scale;
-    T* dk2 = p.dk2 + kbase + (long)kj * rs;
-    T* dv2 = p.dv2 + kbase + (long)kj * rs;
+    T* dk2 = p.dk2 + kbase + (long)kj * rsk;
+    T* dv2 = p.dv2 + kbase + (long)kj * rsk;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
@@ -579,16 +589,16 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
 
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stages) {
-  const int nbh = p.batch * p.heads;
   const int nqb = (p.nq + 32 * kWaves - 1) / (32 * kWaves);
   const int nkb = (p.nk + 32 * kWaves - 1) / (32 * kWaves);
   if (stages & 1) {
-    hipLaunchKernelGGL((bwdbwd_q_kernel<T, D, CAUSAL>), dim3(nqb * nbh), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((bwdbwd_q_kernel<T, D, CAUSAL>), dim3(nqb * p.batch * p.heads), dim3(kThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
-    hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL>), dim3(nkb * nbh), dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL>), dim3(nkb * p.batch * p.kv_heads), dim3(kThreads), 0,
+                       stream, p);
     return hipGetLastError();
   }
   return hipSuccess;

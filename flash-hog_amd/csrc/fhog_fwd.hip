@@ -53,9 +53,11 @@ fwd_kernel(FwdParams<T> p) {
   const int bh = blockIdx.x - rank * nbh;
   const int qb = CAUSAL ? nqb - 1 - rank : rank;
   const int b = bh / p.heads, h = bh % p.heads;
-  const long rs = (long)p.heads * D;
+  const int hk = h / (p.heads / p.kv_heads);
+  const long rs = (long)p.heads * D;      // query-side row stride
+  const long rsk = (long)p.kv_heads * D;  // key-side row stride
   const long qbase = ((long)b * p.nq * p.heads + h) * D;
-  const long kbase = ((long)b * p.nk * p.heads + h) * D;
+  const long kbase = ((long)b * p.nk * p.kv_heads + hk) * D;
   const long sbase = (long)bh * p.nq;
   const int q0 = qb * BQ + wave * 32;
   const int qi = q0 + n;
@@ -68,25 +70,27 @@ fwd_kernel(FwdParams<T> p) {
     qf[ks] = qvalid ? *reinterpret_cast<const V8<T>*>(p.q + off) : zero8<T>();
   }
 
+  // Keys [0, kend) are visible to some query of the workgroup, [0, wend) to
+  // some query of this wave.
   int kend = p.nk;
-  if (CAUSAL) kend = min(kend, qb * BQ + BQ);
+  if (CAUSAL) kend = max(0, min(kend, qb * BQ + BQ + p.coff));
   const int nkt = (kend + BK - 1) / BK;
   int wend = p.nk;
-  if (CAUSAL) wend = min(wend, q0 + 32);
+  if (CAUSAL) wend = max(0, min(wend, q0 + 32 + p.coff));
   const int wkt = q0 < p.nq ? (wend + BK - 1) / BK : 0;
 
   SwzFrags<T, D> fr;
   fr.init(lane);
   const int tensor = wave >> 1;  // 0 = K, 1 = V
   const T* src = (tensor == 0 ? p.k : p.v) + kbase;
-  const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
+  const uint32_t row_bytes = (uint32_t)(rsk * (long)sizeof(T));
   TileDma<T, D, kPer> dma;
   dma.init(row_bytes, BK, lane, kPer * (wave & 1));
   const uint32_t lds_tensor = lds_base_u32(s_kv) + tensor * kTile;
   auto issue = [&](int kt) {
     const int nvalid = p.nk - kt * BK;
     const uint32_t dst = lds_tensor + (uint32_t)((kt % NST) * kStage);
-    const T* gsrc = src + (long)kt * BK * rs;
+    const T* gsrc = src + (long)kt * BK * rsk;
     if (nvalid >= BK) {
       dma.issue(dst, gsrc);
     } else {
@@ -123,8 +127,8 @@ fwd_kernel(FwdParams<T> p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) S[r] *= c2;
       const int k0 = kt * BK;
-      if ((k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0)) {
-        const int klim = min(p.nk - 1, CAUSAL ? qi : p.nk - 1) - k0;  // last visible key, tile-relative
+      if ((k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0 + p.coff)) {
+        const int klim = min(p.nk - 1, CAUSAL ? qi + p.coff : p.nk - 1) - k0;  // last visible key, tile-relative
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           if (crow(r, g) > klim) S[r] = -INFINITY;
@@ -156,9 +160,11 @@ fwd_kernel(FwdParams<T> p) {
     }
   }
 
+  // A query that sees no key (bottom-right causal with nq > nk) gets O = 0 and
+  // L = +inf, so that every backward kernel computes P = exp(S - L) = 0 for it.
   const float l = xgroup_sum(lpart);
   if (qvalid) {
-    const float inv = 1.f / l;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
     T* o = p.o + qbase + (long)qi * rs;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -170,7 +176,7 @@ fwd_kernel(FwdParams<T> p) {
         *reinterpret_cast<V4<T>*>(o + 32 * dt + 8 * a + 4 * g) = cvt4<T>(x);
       }
     }
-    if (g == 0) p.lse[sbase + qi] = (m + __log2f(l)) * kLn2;
+    if (g == 0) p.lse[sbase + qi] = l > 0.f ? (m + __log2f(l)) * kLn2 : INFINITY;
   }
 }
 

@@ -4,6 +4,14 @@
 // Tensors are BTNH (batch, tokens, heads, head_dim) and contiguous, the layout
 // of the reference's attention seam; row statistics are (batch, heads, tokens)
 // fp32, the layout of the reference's logsumexp residual.
+//
+// heads counts query heads (q, o, dout, ddq, dq, dq2, ddo and the row
+// statistics); kv_heads counts key/value heads (k, v, ddk, ddv, dk, dv, dk2,
+// dv2). Query head h reads key/value head h / (heads / kv_heads), the grouping
+// of flash_hog/jax/_pallas_gpu_kernel.py:106-107 ("(kv_heads group)").
+// Causal kernels show key j to query i iff j <= i + coff: coff = 0 aligns the
+// mask top-left (_pallas_gpu_kernel.py:37-41), coff = nk - nq bottom-right
+// (flash_hog/_jax_refs/jax_impl.py:104-109).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -13,7 +21,7 @@ namespace fhog {
 template <typename T> struct FwdParams {
   const T* q; const T* k; const T* v;
   T* o; float* lse;
-  int batch, nq, nk, heads;
+  int batch, nq, nk, heads, kv_heads, coff;
   float scale;
 };
 
@@ -22,7 +30,7 @@ template <typename T> struct BwdParams {
   const float* lse;
   T* dq; T* dk; T* dv;
   float* delta;
-  int batch, nq, nk, heads;
+  int batch, nq, nk, heads, kv_heads, coff;
   float scale;
 };
 
@@ -32,7 +40,7 @@ template <typename T> struct BwdBwdParams {
   const float* lse;
   T* dq2; T* dk2; T* dv2; T* ddo;
   float* delta; float* ddelta; float* bstat;
-  int batch, nq, nk, heads;
+  int batch, nq, nk, heads, kv_heads, coff;
   float scale;
 };
 

@@ -8,6 +8,8 @@ loaded once, and a missing library is an error (there is no fallback path).
 The torch-level helpers below take device tensors, check them, allocate the
 outputs and the fp32 row-statistic workspace with torch's caching allocator,
 and enqueue the kernels on torch's current stream for the tensors' device.
+Their `causal` argument is a bool (top-left when true) or the C ABI's code
+(0 none, 1 top-left, 2 bottom-right).
 """
 
 from __future__ import annotations
@@ -104,15 +106,25 @@ def _check_inputs(named, dtype=None):
 
 
 def _dims(q: torch.Tensor, k: torch.Tensor):
+    """(B, Tq, Tk, N, Nk, H) of q (B, Tq, N, H) and k (B, Tk, Nk, H); N must be a
+    multiple of Nk (grouped-query attention when N > Nk)."""
     if q.ndim != 4 or k.ndim != 4:
         raise ValueError(f"expected (B, T, N, H) tensors, got q{tuple(q.shape)} k{tuple(k.shape)}")
     B, Tq, N, Hd = q.shape
     Bk, Tk, Nk, Hk = k.shape
     if Bk != B or Hk != Hd:
         raise ValueError(f"q{tuple(q.shape)} and k{tuple(k.shape)} disagree on batch or head_dim")
+    if Nk == 0 or N % Nk != 0:
+        raise ValueError(f"query heads ({N}) must be a multiple of key/value heads ({Nk})")
     if q.dtype not in DTYPE_CODES:
         raise ValueError(f"unsupported dtype {q.dtype}")
     return B, Tq, Tk, N, Nk, Hd
+
+
+def causal_code(causal) -> int:
+    """C ABI causal code: False/True map to none/top-left; ints pass through
+    (0 none, 1 top-left, 2 bottom-right; the library rejects others)."""
+    return int(causal)
 
 
 def _expect(name, t, shape, dtype=None):
@@ -122,7 +134,7 @@ def _expect(name, t, shape, dtype=None):
         raise ValueError(f"{name} has dtype {t.dtype}, expected {dtype}")
 
 
-def attention_fwd(q, k, v, causal: bool, scale: float):
+def attention_fwd(q, k, v, causal, scale: float):
     """O (B, T, N, H) in q's dtype and the natural-log logsumexp L (B, N, T) fp32."""
     _check_inputs([("q", q), ("k", k), ("v", v)], q.dtype)
     B, Tq, Tk, N, Nk, Hd = _dims(q, k)
@@ -133,11 +145,11 @@ def attention_fwd(q, k, v, causal: bool, scale: float):
     with torch.cuda.device(q.device):
         check(lib().fhog_attention_fwd(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse),
-            B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], int(bool(causal)), float(scale)))
+            B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], causal_code(causal), float(scale)))
     return o, lse
 
 
-def attention_bwd(q, k, v, o, dout, lse, causal: bool, scale: float):
+def attention_bwd(q, k, v, o, dout, lse, causal, scale: float):
     """dQ, dK, dV of attention given its residual; also returns D (B, N, T) fp32."""
     _check_inputs([("q", q), ("k", k), ("v", v), ("o", o), ("dout", dout)], q.dtype)
     _check_inputs([("q", q), ("lse", lse)])
@@ -153,11 +165,11 @@ def attention_bwd(q, k, v, o, dout, lse, causal: bool, scale: float):
         check(lib().fhog_attention_bwd(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(dout), _ptr(lse),
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta),
-            B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], int(bool(causal)), float(scale)))
+            B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], causal_code(causal), float(scale)))
     return dq, dk, dv, delta
 
 
-def attention_bwdbwd(q, k, v, o, dout, ddq, ddk, ddv, lse, causal: bool, scale: float,
+def attention_bwdbwd(q, k, v, o, dout, ddq, ddk, ddv, lse, causal, scale: float,
                      return_stats: bool = False):
     """dQ2, dK2, dV2, ddO of the double backward [and the row statistics D, dD, B]."""
     _check_inputs([("q", q), ("k", k), ("v", v), ("o", o), ("dout", dout),
@@ -180,7 +192,7 @@ def attention_bwdbwd(q, k, v, o, dout, ddq, ddk, ddv, lse, causal: bool, scale: 
             _ptr(ddq), _ptr(ddk), _ptr(ddv), _ptr(lse),
             _ptr(dq2), _ptr(dk2), _ptr(dv2), _ptr(ddo),
             _ptr(stats[0]), _ptr(stats[1]), _ptr(stats[2]),
-            B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], int(bool(causal)), float(scale)))
+            B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], causal_code(causal), float(scale)))
     if return_stats:
         return dq2, dk2, dv2, ddo, (stats[0], stats[1], stats[2])
     return dq2, dk2, dv2, ddo

@@ -23,63 +23,111 @@ The rules are looked up as module attributes of _attention_impl at call time
 from __future__ import annotations
 
 import torch
+from torch.autograd.function import once_differentiable
 
 from flash_hog._types import MaskType
 from flash_hog.torch import _attention_impl as attn_impl
 
 
-def dot_product_attention(query, key, value, is_causal: bool = False, scale: float | None = None):
+def dot_product_attention(query, key, value, is_causal: bool = False, scale: float | None = None, *,
+                          causal_alignment: str = "top_left"):
     """Softmax attention over (B, T, N, H) or unbatched (T, N, H) tensors.
 
     Dimensions: T query length, S key/value length, N heads, H head dim
-    (flash_hog/jax/attention.py:26-33). scale defaults to H ** -0.5.
+    (flash_hog/jax/attention.py:26-33). scale defaults to H ** -0.5. key and
+    value may have fewer heads than query (a divisor: grouped-query attention,
+    query head n uses key/value head n // (N / N_kv)).
+
+    causal_alignment (an addition to the reference's signature) places the
+    causal diagonal: "top_left" (key s visible to query t iff s <= t, the
+    reference kernel's mask) or "bottom_right" (s <= t + S - T, the mask of
+    flash_hog/_jax_refs/jax_impl.py:104-109); they agree when T == S.
     """
     if scale is None:
         scale = query.shape[-1] ** -0.5
     dtype = query.dtype
     if not (dtype == key.dtype == value.dtype):
         raise ValueError(f"query, key and value must share a dtype, got {query.dtype}, {key.dtype}, {value.dtype}")
-    mask_type = MaskType.CAUSAL if is_causal else MaskType.NO_MASK
+    if causal_alignment not in ("top_left", "bottom_right"):
+        raise ValueError(f"causal_alignment must be 'top_left' or 'bottom_right', got {causal_alignment!r}")
+    if not is_causal:
+        mask_type = MaskType.NO_MASK
+    elif causal_alignment == "top_left":
+        mask_type = MaskType.CAUSAL
+    else:
+        mask_type = MaskType.CAUSAL_BOTTOM_RIGHT
     unbatched = query.ndim == 3
     if unbatched:
         query, key, value = query.unsqueeze(0), key.unsqueeze(0), value.unsqueeze(0)
-    result = _DotProductAttention.apply(query, key, value, mask_type, float(scale))
+    result, _ = _DotProductAttention.apply(query, key, value, mask_type, float(scale))
     if unbatched:
         result = result.squeeze(0)
     return result
 
 
+# Both Functions keep their residuals among their inputs and outputs and save
+# them in setup_context, so torch.func transforms (vmap, grad, jacrev) compose
+# with them; under vmap the kernels' own vmap rules fold the mapped axis into
+# the batch axis (flash_hog/torch/_hip_gpu.py).
+
 class _DotProductAttention(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, query, key, value, mask_type, scale):
-        out, res = attn_impl.dot_product_attention_fwd_rule(query, key, value, mask_type=mask_type, scale=scale)
-        q, k, v, activation, o = res
-        ctx.save_for_backward(q, k, v, activation, o.detach())
-        ctx.mask_type = mask_type
-        ctx.scale = scale
-        return out
+    """Primal: (q, k, v) -> (O, L); L = activation, the fwd rule's residual
+    (attention.py:64-72), is returned so that it can be saved, and is not
+    differentiable."""
+
+    generate_vmap_rule = True
 
     @staticmethod
-    def backward(ctx, g):
+    def forward(query, key, value, mask_type, scale):
+        out, (_, _, _, activation, _) = attn_impl.dot_product_attention_fwd_rule(
+            query, key, value, mask_type=mask_type, scale=scale)
+        return out, activation
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        query, key, value, mask_type, scale = inputs
+        out, activation = output
+        # the residual (q, k, v, L, O) of dot_product_attention_fwd_rule
+        ctx.save_for_backward(query, key, value, activation, out)
+        ctx.mark_non_differentiable(activation)
+        ctx.mask_type = mask_type
+        ctx.scale = scale
+
+    @staticmethod
+    def backward(ctx, g, _g_activation):
         q, k, v, activation, o = ctx.saved_tensors
-        dq, dk, dv = _DotProductAttentionBwd.apply(ctx.mask_type, ctx.scale, q, k, v, activation, o, g)
+        # O enters the first backward as a constant (the double-backward rule
+        # returns no cotangent for it); detaching it keeps this node out of the
+        # graph of a second derivative, which would otherwise call it again with
+        # a zero cotangent.
+        dq, dk, dv = _DotProductAttentionBwd.apply(ctx.mask_type, ctx.scale, q, k, v, activation, o.detach(), g)
         return dq, dk, dv, None, None
 
 
 class _DotProductAttentionBwd(torch.autograd.Function):
     """Primal: (q, k, v, L, O, dO) -> (dQ, dK, dV); differentiable in q, k, v, dO."""
 
+    generate_vmap_rule = True
+
     @staticmethod
-    def forward(ctx, mask_type, scale, query, key, value, activation, out, g):
-        (dq, dk, dv), residual = attn_impl.dot_product_attention_bwd_rule_fwd_rule(
+    def forward(mask_type, scale, query, key, value, activation, out, g):
+        (dq, dk, dv), _ = attn_impl.dot_product_attention_bwd_rule_fwd_rule(
             mask_type=mask_type, scale=scale, res=(query, key, value, activation, out), g=g)
-        ctx.save_for_backward(*residual)
-        ctx.mask_type = mask_type
-        ctx.scale = scale
         return dq, dk, dv
 
     @staticmethod
+    def setup_context(ctx, inputs, output):
+        mask_type, scale, query, key, value, activation, out, g = inputs
+        # the residual (q, k, v, O, L, dO) of dot_product_attention_bwd_rule_fwd_rule
+        ctx.save_for_backward(query, key, value, out, activation, g)
+        ctx.mask_type = mask_type
+        ctx.scale = scale
+
+    @staticmethod
+    @once_differentiable
     def backward(ctx, ddq, ddk, ddv):
+        # The rules stop at second order (as the reference's do): the outputs
+        # of this backward raise if differentiated again.
         res = ctx.saved_tensors
         (dq2, dk2, dv2, _, _), ddo = attn_impl.dot_product_attention_bwd_rule_bwd_rule(
             mask_type=ctx.mask_type, scale=ctx.scale, res=res, g=(ddq, ddk, ddv))

@@ -10,16 +10,26 @@
  *
  * Layouts (identical to the reference's attention seam):
  *   q, o, dout, ddq, dq, dq2, ddo   : (batch, n_q, heads, head_dim) contiguous
- *   k, v, ddk, ddv, dk, dv, dk2, dv2: (batch, n_k, heads, head_dim) contiguous
+ *   k, v, ddk, ddv, dk, dv, dk2, dv2: (batch, n_k, kv_heads, head_dim) contiguous
  *   lse, delta, ddelta, bstat       : (batch, heads, n_q) fp32 contiguous
  * lse is the natural-log logsumexp of the scaled, masked logits
- * (flash_hog/jax/_pallas_gpu_kernel.py:97). Causal masking is top-left
- * aligned: query i attends to keys j <= i (_pallas_gpu_kernel.py:37-41).
+ * (flash_hog/jax/_pallas_gpu_kernel.py:97).
+ *
+ * Grouped-query attention: heads must be a multiple of kv_heads; query head h
+ * attends with key/value head h / (heads / kv_heads), and dk, dv, dk2, dv2 sum
+ * over the heads of a group (_pallas_gpu_kernel.py:99, 106-107, 333-370).
+ *
+ * causal (enum fhog_causal): FHOG_CAUSAL_TOP_LEFT shows key j to query i iff
+ * j <= i (_pallas_gpu_kernel.py:37-41, the reference kernel's mask);
+ * FHOG_CAUSAL_BOTTOM_RIGHT iff j <= i + n_k - n_q
+ * (flash_hog/_jax_refs/jax_impl.py:104-109); the two agree when n_q == n_k.
+ * A query that sees no key (bottom-right with n_q > n_k) gets o = 0,
+ * lse = +inf and zero gradients.
  * Tensor pointers must be 16-byte aligned, row-statistic pointers 4-byte aligned.
  *
  * Supported: dtype FHOG_DTYPE_{BF16,F16} with head_dim 64 or 128,
  * FHOG_DTYPE_F32 with head_dim 64; any n_q, n_k >= 1 (ragged tails are
- * masked); heads == kv_heads.
+ * masked).
  */
 #ifndef FLASH_HOG_H_
 #define FLASH_HOG_H_
@@ -41,6 +51,9 @@ enum fhog_status {
 };
 
 enum fhog_dtype { FHOG_DTYPE_F32 = 0, FHOG_DTYPE_F16 = 1, FHOG_DTYPE_BF16 = 2 };
+
+/* Values of the `causal` argument. */
+enum fhog_causal { FHOG_CAUSAL_NONE = 0, FHOG_CAUSAL_TOP_LEFT = 1, FHOG_CAUSAL_BOTTOM_RIGHT = 2 };
 
 /* Version of this ABI (major * 100 + minor). */
 int fhog_abi_version(void);

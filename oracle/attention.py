@@ -15,14 +15,24 @@ matrix, one (batch, head) at a time:
                       flash_hog/jax/_pallas_gpu_kernel.py:110, :168, :209-210
 
 Layouts follow the reference's seam: q, k, v and friends are (B, T, H, D)
-arrays, L is (B, H, T). Causal masking is top-left aligned, key j visible to
-query i iff j <= i (flash_hog/jax/_pallas_gpu_kernel.py:37-41); jax_impl.py's
-get_mask_bottom_right (:104-109) is identical to it whenever N_Q == N_K.
+arrays, L is (B, H, T). `causal` is False/0 (no mask), True/1 (top-left: key j
+visible to query i iff j <= i, flash_hog/jax/_pallas_gpu_kernel.py:37-41) or 2
+(bottom-right: j <= i + N_K - N_Q, jax_impl.py:104-109 get_mask_bottom_right
+with an infinite window); the two agree whenever N_Q == N_K. A query that sees
+no key (bottom-right, N_Q > N_K) gets O = 0, L = +inf and zero gradients; the
+reference's softmax leaves such rows undefined (NaN).
+
+Grouped-query attention: k, v, ddk, ddv may have fewer heads than q (a
+divisor); query head h uses key/value head h // (H_q / H_kv), the grouping
+"(kv_heads group)" of _pallas_gpu_kernel.py:106-107, and the key-side
+gradients sum over the heads of a group (_pallas_gpu_kernel.py:333-370).
 
 How each function is pinned (tests/test_oracle.py):
   attn_fwd            torch.nn.functional.scaled_dot_product_attention and
-                      torch.logsumexp (library routines); row sums of P == 1;
-                      causal row 0 reproduces V_0.
+                      torch.logsumexp (library routines), including its
+                      enable_gqa head grouping and its bottom-right causal bias
+                      (torch.nn.attention.bias.causal_lower_right); row sums of
+                      P == 1; causal row 0 reproduces V_0.
   attn_bwd            torch autograd of textbook attention (fp64); sum over keys
                       of dK == 0.
   attn_bwd_bwd_stats  the reference's golden vectors (test_data.zip);
@@ -33,6 +43,13 @@ How each function is pinned (tests/test_oracle.py):
                       the causal prefix property.
   row statistics      D against rowsum(P * dP); dD, B against their definitions
                       through the autograd double backward's outputs.
+  grouped heads       the outputs equal those of the ungrouped problem with
+                      k, v, ddk, ddv repeated per group and the key-side
+                      gradients summed over the group; torch autograd (fp64)
+                      of SDPA with enable_gqa for the first backward.
+  empty rows          rows that see no key contribute nothing: a bottom-right
+                      run with N_Q > N_K equals, on its last N_K rows and on
+                      every key-side output, the square run of those rows.
 """
 
 from __future__ import annotations
@@ -49,21 +66,23 @@ def _bthd(x: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(np.transpose(x, (0, 2, 1, 3)))
 
 
-def causal_mask(n_q: int, n_k: int) -> np.ndarray:
-    """Boolean (n_q, n_k): key j visible to query i iff j <= i (top-left)."""
-    return np.arange(n_k)[None, :] <= np.arange(n_q)[:, None]
+def causal_mask(n_q: int, n_k: int, causal=1) -> np.ndarray:
+    """Boolean (n_q, n_k): key j visible to query i iff j <= i (causal 1,
+    top-left) or j <= i + n_k - n_q (causal 2, bottom-right)."""
+    off = n_k - n_q if int(causal) == 2 else 0
+    return np.arange(n_k)[None, :] <= np.arange(n_q)[:, None] + off
 
 
-def _scores(q: np.ndarray, k: np.ndarray, scale: float, causal: bool) -> np.ndarray:
+def _scores(q: np.ndarray, k: np.ndarray, scale: float, causal) -> np.ndarray:
     s = scale * (q @ k.T)
     if causal:
-        s = np.where(causal_mask(q.shape[0], k.shape[0]), s, -np.inf)
+        s = np.where(causal_mask(q.shape[0], k.shape[0], causal), s, -np.inf)
     return s
 
 
 def _probs(q, k, lse, scale, causal):
     s = _scores(q, k, scale, causal)
-    return np.exp(s - lse[:, None])
+    return np.exp(s - lse[:, None])  # masked entries and empty rows (L = +inf) give 0
 
 
 # --------------------------------------------------------------------------
@@ -74,10 +93,13 @@ def fwd_head(q, k, v, scale, causal):
     """O and natural-log L of one head (jax_impl.py:112-139, :423)."""
     s = _scores(q, k, scale, causal)
     m = np.max(s, axis=-1, keepdims=True)
+    empty = np.isneginf(m)  # rows that see no key
+    m = np.where(empty, 0.0, m)
     e = np.exp(s - m)
     z = np.sum(e, axis=-1, keepdims=True)
-    lse = (m + np.log(z))[:, 0]
-    return (e / z) @ v, lse
+    zs = np.where(empty, 1.0, z)
+    lse = np.where(empty, np.inf, m + np.log(zs))[:, 0]
+    return (e / zs) @ v, lse
 
 
 def bwd_head(q, k, v, o, do, lse, scale, causal):
@@ -116,46 +138,63 @@ def bwd_bwd_head(q, k, v, o, do, ddq, ddk, ddv, lse, scale, causal):
 # batched (B, T, H, D) wrappers
 # --------------------------------------------------------------------------
 
-def attn_fwd(q, k, v, scale: float, causal: bool):
+def _group(Q: np.ndarray, K: np.ndarray) -> int:
+    """Query heads per key/value head of (B, H, T, D) arrays."""
+    H, Hk = Q.shape[1], K.shape[1]
+    if H % Hk:
+        raise ValueError(f"query heads ({H}) must be a multiple of key/value heads ({Hk})")
+    return H // Hk
+
+
+def attn_fwd(q, k, v, scale: float, causal):
     """Returns O (B, T, H, D) and L (B, H, T), float64."""
     Q, K, V = _bhtd(q), _bhtd(k), _bhtd(v)
     B, H, T, _ = Q.shape
+    G = _group(Q, K)
     O = np.empty((B, H, T, V.shape[-1]))
     L = np.empty((B, H, T))
     for b in range(B):
         for h in range(H):
-            O[b, h], L[b, h] = fwd_head(Q[b, h], K[b, h], V[b, h], scale, causal)
+            O[b, h], L[b, h] = fwd_head(Q[b, h], K[b, h // G], V[b, h // G], scale, causal)
     return _bthd(O), L
 
 
-def attn_bwd(q, k, v, o, do, lse, scale: float, causal: bool):
+def attn_bwd(q, k, v, o, do, lse, scale: float, causal):
     """Returns dQ, dK, dV (B, T, H, D) and D (B, H, T), float64."""
     Q, K, V, O, dO = (_bhtd(x) for x in (q, k, v, o, do))
     Ls = np.asarray(lse, dtype=np.float64)
     B, H = Q.shape[:2]
-    dQ, dK, dV = np.empty_like(Q), np.empty_like(K), np.empty_like(V)
+    G = _group(Q, K)
+    dQ, dK, dV = np.empty_like(Q), np.zeros_like(K), np.zeros_like(V)
     Dv = np.empty(Ls.shape)
     for b in range(B):
         for h in range(H):
-            dQ[b, h], dK[b, h], dV[b, h], Dv[b, h] = bwd_head(
-                Q[b, h], K[b, h], V[b, h], O[b, h], dO[b, h], Ls[b, h], scale, causal)
+            dq, dk, dv, Dv[b, h] = bwd_head(
+                Q[b, h], K[b, h // G], V[b, h // G], O[b, h], dO[b, h], Ls[b, h], scale, causal)
+            dQ[b, h] = dq
+            dK[b, h // G] += dk
+            dV[b, h // G] += dv
     return _bthd(dQ), _bthd(dK), _bthd(dV), Dv
 
 
-def attn_bwd_bwd_stats(q, k, v, o, do, ddq, ddk, ddv, lse, scale: float, causal: bool,
+def attn_bwd_bwd_stats(q, k, v, o, do, ddq, ddk, ddv, lse, scale: float, causal,
                        return_stats: bool = False):
     """Returns dQ2, dK2, dV2, ddO (B, T, H, D) float64 [and D, dD, B (B, H, T)]."""
     Q, K, V, O, dO, ddQ, ddK, ddV = (_bhtd(x) for x in (q, k, v, o, do, ddq, ddk, ddv))
     Ls = np.asarray(lse, dtype=np.float64)
     B, H = Q.shape[:2]
-    dQ2, dK2, dV2, ddO = np.empty_like(Q), np.empty_like(K), np.empty_like(V), np.empty_like(O)
+    G = _group(Q, K)
+    dQ2, dK2, dV2, ddO = np.empty_like(Q), np.zeros_like(K), np.zeros_like(V), np.empty_like(O)
     Dv, dDv, Bv = np.empty(Ls.shape), np.empty(Ls.shape), np.empty(Ls.shape)
     for b in range(B):
         for h in range(H):
-            (dQ2[b, h], dK2[b, h], dV2[b, h], ddO[b, h],
+            hk = h // G
+            (dQ2[b, h], dk2, dv2, ddO[b, h],
              Dv[b, h], dDv[b, h], Bv[b, h]) = bwd_bwd_head(
-                Q[b, h], K[b, h], V[b, h], O[b, h], dO[b, h],
-                ddQ[b, h], ddK[b, h], ddV[b, h], Ls[b, h], scale, causal)
+                Q[b, h], K[b, hk], V[b, hk], O[b, h], dO[b, h],
+                ddQ[b, h], ddK[b, hk], ddV[b, hk], Ls[b, h], scale, causal)
+            dK2[b, hk] += dk2
+            dV2[b, hk] += dv2
     outs = (_bthd(dQ2), _bthd(dK2), _bthd(dV2), _bthd(ddO))
     if return_stats:
         return outs + (Dv, dDv, Bv)

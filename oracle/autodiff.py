@@ -20,12 +20,23 @@ import math
 import torch
 
 
-def attention(q, k, v, scale: float, causal: bool):
-    """Textbook attention on (B, T, H, D) tensors, top-left causal mask."""
+def attention(q, k, v, scale: float, causal):
+    """Textbook attention on (B, T, H, D) tensors.
+
+    causal: False/0 none, True/1 top-left (key j visible to query i iff
+    j <= i), 2 bottom-right (j <= i + n_k - n_q). k and v may have fewer heads
+    than q (a divisor): they are repeated per group of consecutive query heads
+    (torch.repeat_interleave, the grouping of SDPA's enable_gqa), so autograd
+    sums the key-side gradients over each group.
+    """
+    G = q.shape[2] // k.shape[2]
+    if G > 1:
+        k, v = k.repeat_interleave(G, dim=2), v.repeat_interleave(G, dim=2)
     s = torch.einsum("bqhd,bkhd->bhqk", q, k) * scale
     if causal:
         nq, nk = q.shape[1], k.shape[1]
-        mask = torch.arange(nk)[None, :] <= torch.arange(nq)[:, None]
+        off = nk - nq if int(causal) == 2 else 0
+        mask = torch.arange(nk)[None, :] <= torch.arange(nq)[:, None] + off
         s = s.masked_fill(~mask, float("-inf"))
     p = torch.softmax(s, dim=-1)
     return torch.einsum("bhqk,bkhd->bqhd", p, v)
@@ -58,12 +69,19 @@ def double_vjp_chunked(q, k, v, do, ddq, ddk, ddv, scale: float, causal: bool, h
     return tuple(outs)
 
 
-def unmasked_pairs(n_q: int, n_k: int, causal: bool) -> int:
-    """Number of (query, key) pairs that survive the mask, per (batch, head)."""
+def unmasked_pairs(n_q: int, n_k: int, causal) -> int:
+    """Number of (query, key) pairs that survive the mask, per (batch, head):
+    query i sees min(n_k, max(0, i + 1 + off)) keys, off = 0 top-left (causal
+    1 or True), n_k - n_q bottom-right (causal 2)."""
     if not causal:
         return n_q * n_k
-    full = min(n_q, n_k)
-    return full * (full + 1) // 2 + max(0, n_q - n_k) * n_k
+    off = n_k - n_q if int(causal) == 2 else 0
+    # sum over i of clamp(i + 1 + off, 0, n_k): a ramp, then a plateau at n_k
+    lo = max(0, -off)                     # first query that sees a key
+    ramp_end = min(n_q, max(lo, n_k - off - 1))  # queries [lo, ramp_end) see i + 1 + off < n_k keys
+    a, b = lo + 1 + off, ramp_end + off   # first and last ramp counts
+    ramp = (a + b) * (ramp_end - lo) // 2 if ramp_end > lo else 0
+    return ramp + (n_q - ramp_end) * n_k
 
 
 def bwdbwd_algorithmic_flops(batch, heads, n_q, n_k, head_dim, causal) -> float:

@@ -15,17 +15,19 @@ TOL = {torch.float32: 1e-3, torch.float16: 2e-2, torch.bfloat16: 2e-2}
 TENSOR_ORDER = ("q", "k", "v", "do", "ddq", "ddk", "ddv")
 
 
-def make_inputs(batch, n_q, n_k, heads, head_dim, dtype, seed=0, qkv_scale=1.0, device="cpu"):
+def make_inputs(batch, n_q, n_k, heads, head_dim, dtype, seed=0, qkv_scale=1.0, device="cpu", kv_heads=None):
     """Seeded N(0, 1) inputs in (B, T, N, H) layout, rounded to dtype.
 
     Tensor i of TENSOR_ORDER is drawn from torch.Generator seeded with seed + i;
-    q, k, v are multiplied by qkv_scale before rounding.
+    q, k, v are multiplied by qkv_scale before rounding. k, v, ddk, ddv have
+    kv_heads heads (default: heads).
     """
+    kv_heads = heads if kv_heads is None else kv_heads
     shapes = {"q": (batch, n_q, heads, head_dim), "do": (batch, n_q, heads, head_dim),
               "ddq": (batch, n_q, heads, head_dim)}
     out = {}
     for i, name in enumerate(TENSOR_ORDER):
-        shape = shapes.get(name, (batch, n_k, heads, head_dim))
+        shape = shapes.get(name, (batch, n_k, kv_heads, head_dim))
         gen = torch.Generator().manual_seed(seed + i)
         x = torch.randn(shape, generator=gen, dtype=torch.float32)
         if name in ("q", "k", "v"):

@@ -47,7 +47,7 @@ def test_python_signatures_cover_the_header():
 
 
 def test_status_strings(lib):
-    assert lib.fhog_abi_version() == 100
+    assert lib.fhog_abi_version() == 101
     assert lib.fhog_status_string(0) == b"ok"
     assert lib.fhog_status_string(1) == b"invalid argument"
     assert lib.fhog_status_string(2) == b"unsupported"
@@ -72,7 +72,8 @@ def _bwdbwd_args(ptr=16, batch=1, n_q=16, n_k=16, heads=1, kv_heads=1, head_dim=
     (dict(n_k=0), 1, "sizes must be >= 1"),
     (dict(dtype=7), 1, "unknown dtype"),
     (dict(heads=3, kv_heads=2), 1, "multiple of kv_heads"),
-    (dict(heads=4, kv_heads=2), 2, "grouped-query"),
+    (dict(causal=3), 1, "causal must be 0 (none), 1 (top-left) or 2 (bottom-right)"),
+    (dict(causal=-1), 1, "causal must be"),
     (dict(head_dim=96), 2, "head_dim must be 64 or 128"),
     (dict(head_dim=128, dtype=0), 2, "fp32 supports head_dim 64"),
     (dict(scale=float("nan")), 1, "scale"),

@@ -18,11 +18,11 @@ from oracle import autodiff
 pytestmark = pytest.mark.gpu
 
 
-def fhog_bwd_bwd(q, k, v, do, ddq, ddk, ddv, is_causal, scale):
+def fhog_bwd_bwd(q, k, v, do, ddq, ddk, ddv, is_causal, scale, **kw):
     import flash_hog
 
     q, k, v, do = (t.detach().requires_grad_(True) for t in (q, k, v, do))
-    out = flash_hog.dot_product_attention(q, k, v, is_causal=is_causal, scale=scale)
+    out = flash_hog.dot_product_attention(q, k, v, is_causal=is_causal, scale=scale, **kw)
     dq, dk, dv = torch.autograd.grad(out, (q, k, v), do, create_graph=True)
     return torch.autograd.grad((dq, dk, dv), (q, k, v, do), (ddq, ddk, ddv)), (out, dq, dk, dv)
 
@@ -78,3 +78,77 @@ def test_hvp_matches_double_vjp(cuda_device):
     ref = autodiff.double_vjp(c["q"], c["k"], c["v"], c["do"], c["ddq"], c["ddk"], c["ddv"], 0.125, True)
     for a, r in zip(hvp, ref[:3]):
         assert rel_err(a, r) < 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+@pytest.mark.parametrize("nq,nk,heads,kv_heads,alignment", [
+    (96, 160, 4, 2, "bottom_right"),
+    (160, 96, 6, 2, "bottom_right"),
+    (128, 128, 8, 1, "top_left"),
+], ids=["br_short_q_gqa2", "br_long_q_gqa3", "mqa_top_left"])
+def test_backward_backward_gqa_and_alignment(nq, nk, heads, kv_heads, alignment, dtype, cuda_device):
+    """Grad-of-grad with grouped key/value heads and either causal alignment,
+    against the fp64 autograd oracle with the same grouping and mask."""
+    print("[case] frontend grad-of-grad", dtype, nq, nk, heads, kv_heads, alignment, flush=True)
+    x = make_inputs(2, nq, nk, heads, 64, dtype, seed=44, kv_heads=kv_heads)
+    scale = default_scale(64)
+    code = 2 if alignment == "bottom_right" else 1
+    dev = {n: t.to(cuda_device) for n, t in x.items()}
+    (dq2, dk2, dv2, ddo), (out, dq, dk, dv) = fhog_bwd_bwd(
+        dev["q"], dev["k"], dev["v"], dev["do"], dev["ddq"], dev["ddk"], dev["ddv"], True, scale,
+        causal_alignment=alignment)
+    torch.cuda.synchronize()
+    c = {n: t.double() for n, t in x.items()}
+    ref2 = autodiff.double_vjp(c["q"], c["k"], c["v"], c["do"], c["ddq"], c["ddk"], c["ddv"], scale, code)
+    ref1 = autodiff.first_vjp(c["q"], c["k"], c["v"], c["do"], scale, code)
+    ref_out = autodiff.attention(c["q"], c["k"], c["v"], scale, code)
+    if nq > nk:  # rows without keys: the oracle's softmax gives NaN there, the kernels zeros
+        e = nq - nk
+        assert torch.all(out[:, :e] == 0) and torch.all(dq[:, :e] == 0)
+        assert torch.all(dq2[:, :e] == 0) and torch.all(ddo[:, :e] == 0)
+        ref_out = ref_out.nan_to_num(0.0)
+        # key-side and remaining rows: the square problem made of the last nk queries
+        sq = {n: (t[:, e:] if n in ("q", "do", "ddq") else t) for n, t in c.items()}
+        ref2 = autodiff.double_vjp(sq["q"], sq["k"], sq["v"], sq["do"], sq["ddq"], sq["ddk"], sq["ddv"], scale, 1)
+        ref1 = autodiff.first_vjp(sq["q"], sq["k"], sq["v"], sq["do"], scale, 1)
+        dq, dq2, ddo = dq[:, e:], dq2[:, e:], ddo[:, e:]
+    assert rel_err(out, ref_out) < TOL[dtype]
+    for a, r, n in zip((dq, dk, dv), ref1, ("dq", "dk", "dv")):
+        assert rel_err(a, r) < TOL[dtype], n
+    for a, r, n in zip((dq2, dk2, dv2, ddo), ref2, ("dq2", "dk2", "dv2", "ddo")):
+        assert rel_err(a, r) < TOL[dtype], n
+
+
+def test_vmap_hvp_equals_folded_batch(cuda_device):
+    """torch.func.vmap of a per-example Hessian-vector product folds the mapped
+    axis into the batch axis (one kernel call per rule), so it equals, bit for
+    bit, the batched computation on the folded tensors."""
+    import flash_hog
+
+    print("[case] frontend vmap hvp", flush=True)
+    V, B, N, H, Hk, D = 3, 2, 128, 4, 2, 64
+    x = make_inputs(V * B, N, N, H, D, torch.bfloat16, seed=51, kv_heads=Hk)
+    dev = {n: t.to(cuda_device) for n, t in x.items()}
+
+    def loss(q, k, v, w):
+        return (flash_hog.dot_product_attention(q, k, v, is_causal=True).float() * w.float()).sum()
+
+    def g_dot_u(q, k, v, w, uq, uk, uv):
+        gr = torch.func.grad(loss, argnums=(0, 1, 2))(q, k, v, w)
+        return sum((a.float() * b.float()).sum() for a, b in zip(gr, (uq, uk, uv)))
+
+    hvp = torch.func.grad(g_dot_u, argnums=(0, 1, 2))
+    unfold = lambda t: t.unflatten(0, (V, B))
+    args = [dev[n] for n in ("q", "k", "v", "do", "ddq", "ddk", "ddv")]
+    mapped = torch.func.vmap(hvp)(*(unfold(t) for t in args))
+    folded = hvp(*args)
+    torch.cuda.synchronize()
+    for a, b in zip(mapped, folded):
+        assert torch.equal(a.flatten(0, 1), b)
+    # an unmapped key/value pair is broadcast along the mapped axis
+    kv = dict(in_dims=(0, None, None, 0))
+    out = torch.func.vmap(lambda q, k, v, w: flash_hog.dot_product_attention(q, k, v, is_causal=True), **kv)(
+        unfold(dev["q"]), dev["k"][:B], dev["v"][:B], unfold(dev["do"]))
+    ref = flash_hog.dot_product_attention(dev["q"], dev["k"][:B].repeat(V, 1, 1, 1), dev["v"][:B].repeat(V, 1, 1, 1),
+                                          is_causal=True)
+    assert torch.equal(out.flatten(0, 1), ref)
