@@ -24,7 +24,8 @@ shapes of the reference's HVP tables (flash_hog/csrc/tk_bwdbwd/BENCHMARKS.md:
 12 heads, head_dim 64, causal, fp32 inputs cast to bf16 around the attention
 call; "b1" = batch 1 at sequence 512 ... 131072, "tokens" = batch x sequence
 = 262144). Prints one markdown row per shape on stderr and one JSON line per
-shape on stdout.
+shape on stdout. Up to sequence 4096 the HVP is also captured in a HIP graph
+(torch.cuda.graph) and the mean replay time reported beside the eager time.
 """
 
 from __future__ import annotations
@@ -121,6 +122,8 @@ def cpu_baseline(args, B, N, H, D, scale, causal):
     }
 
 
+GRAPH_MAX_SEQ = 4096  # graph replay is also timed up to this sequence length (host overhead matters there)
+
 HVP_TABLES = {
     "b1": [(1, 512 << i) for i in range(9)],
     "tokens": [(262144 // (512 << i), 512 << i) for i in range(9)],
@@ -162,6 +165,35 @@ def hvp_table(args):
         g = torch.autograd.grad(loss, x, create_graph=True)
         return torch.autograd.grad(g, x, tan)
 
+    def hvp_vjp(attn, x, cot, tan):
+        """The same HVP as two vector-Jacobian products (no reduction), for graph capture."""
+        x = [t.detach().requires_grad_(True) for t in x]
+        g = torch.autograd.grad(attn(*x), x, cot, create_graph=True)
+        return torch.autograd.grad(g, x, tan)
+
+    def graph_ms(f, x, cot, tan, iters):
+        """Mean replay time of the HVP captured in a HIP graph (torch.cuda.graph)."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                hvp_vjp(f, x, cot, tan)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = hvp_vjp(f, x, cot, tan)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        del graph, out
+        return e0.elapsed_time(e1) / iters
+
     def compare(a, r):
         a = torch.cat([t.double().flatten() for t in a])
         r = torch.cat([t.double().flatten() for t in r])
@@ -169,8 +201,8 @@ def hvp_table(args):
         return cos, float((a - r).abs().max() / r.abs().max())
 
     rows = []
-    log("| batch | seq | HVP (ms) | faithfulness |")
-    log("|--:|--:|--:|:--|")
+    log("| batch | seq | HVP (ms) | HVP, graph replay (ms) | faithfulness |")
+    log("|--:|--:|--:|--:|:--|")
     for B, N in HVP_TABLES[args.hvp_table]:
         gen = torch.Generator().manual_seed(B * 7919 + N)
         mk = lambda: torch.randn((B, N, H, D), generator=gen).to(dev)
@@ -187,6 +219,7 @@ def hvp_table(args):
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / iters
+        gms = graph_ms(f, x, cot, tan, iters) if N <= GRAPH_MAX_SEQ else None
         if B * N * N <= 2048 * 2048:
             ref, against = hvp(attn_dense, x, cot, tan), "dense fp32"
         elif N <= 16384:
@@ -195,13 +228,14 @@ def hvp_table(args):
             ref, against = None, None
         faith = "not measured"
         row = {"table": args.hvp_table, "batch": B, "seq": N, "heads": H, "head_dim": D, "hvp_ms": round(ms, 4),
-               "iterations": iters}
+               "hvp_graph_ms": None if gms is None else round(gms, 4), "iterations": iters}
         if ref is not None:
             cos, rel = compare(out, ref)
             faith = f"cos {cos:.4f}, max rel err {rel:.1e} vs {against}"
             row.update(cos=round(cos, 6), max_rel_err=rel, against=against)
         torch.cuda.synchronize()
-        log(f"| {B} | {N} | {ms:.2f} | {faith} |")
+        gtxt = "-" if gms is None else f"{gms:.2f}"
+        log(f"| {B} | {N} | {ms:.2f} | {gtxt} | {faith} |")
         print(json.dumps(row), flush=True)
         rows.append(row)
         del x, cot, tan, out, ref
