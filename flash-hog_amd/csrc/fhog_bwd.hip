@@ -87,8 +87,9 @@ bwd_q_kernel(BwdParams<T> p) {
   const float nL2 = qvalid ? -p.lse[sbase + qi] * kLog2e : 0.f;
 
   int kend = p.nk;
-  if (CAUSAL) kend = max(0, min(kend, qb * BQ + BQ + p.coff));
-  const int nkt = (kend + BK - 1) / BK;
+  if (CAUSAL) kend = min(kend, qb * BQ + BQ + p.coff);
+  // (uniform; saying so keeps the compiler from treating the loop as divergent)
+  const int nkt = __builtin_amdgcn_readfirstlane(kend > 0 ? (kend + BK - 1) / BK : 0);
   int wend = p.nk;
   if (CAUSAL) wend = max(0, min(wend, q0 + 32 + p.coff));
   const int wkt = q0 < p.nq ? (wend + BK - 1) / BK : 0;
@@ -248,13 +249,12 @@ bwd_k_kernel(BwdParams<T> p) {
     TileDma<T, D, kPer> dma;
     dma.init(row_bytes, BQ, lane, kPer * (wave & 1));
     const uint32_t lds0 = lds_base_u32(s_q);
-    auto issue = [&](int i) {
-      const int qt = i / grp, gi = i - qt * grp;
-      const int q0t = (qt_begin + qt) * BQ;
+    auto issue = [&](int i, GroupCursor c) {
+      const int q0t = (qt_begin + c.qt) * BQ;
       const uint32_t stage = lds0 + (uint32_t)((i % NST) * kStage);
       const int nvalid = p.nq - q0t;
-      const T* gsrc = src + (long)gi * D + (long)q0t * rs;
-      const long sb = sbase + (long)gi * p.nq;
+      const T* gsrc = src + (long)c.gi * D + (long)q0t * rs;
+      const long sb = sbase + (long)c.gi * p.nq;
       if (nvalid >= BQ) {
         dma.issue(stage + tensor * kTile, gsrc);
       } else {
@@ -286,16 +286,24 @@ bwd_k_kernel(BwdParams<T> p) {
 
     // Retire the key-side loads before the ring starts (see fwd_kernel).
     wait_vmem();
+    GroupCursor nxt;  // iteration of the next tile to issue
 #pragma unroll
     for (int i = 0; i < NST - 1; ++i)
-      if (i < total) issue(i);
+      if (i < total) {
+        issue(i, nxt);
+        nxt.next(grp);
+      }
 
-    for (int i = 0; i < total; ++i) {
+    GroupCursor cur;  // iteration i
+    for (int i = 0; i < total; ++i, cur.next(grp)) {
       wait_for(i);
       finish_stats(i);
       __syncthreads();
-      if (i + NST - 1 < total) issue(i + NST - 1);
-      const int q0 = (qt_begin + i / grp) * BQ;
+      if (i + NST - 1 < total) {
+        issue(i + NST - 1, nxt);
+        nxt.next(grp);
+      }
+      const int q0 = (qt_begin + cur.qt) * BQ;
       const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
       if (active) {
         const char* st = s_q + (i % NST) * kStage;

@@ -129,8 +129,9 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   const float nL2 = qvalid ? -p.lse[sbase + qi] * kLog2e : 0.f;
 
   int kend = p.nk;
-  if (CAUSAL) kend = max(0, min(kend, qb * BQ + BQ + p.coff));
-  const int nkt = (kend + BK - 1) / BK;                   // tiles the workgroup streams
+  if (CAUSAL) kend = min(kend, qb * BQ + BQ + p.coff);
+  // (uniform; saying so keeps the compiler from treating the loops as divergent)
+  const int nkt = __builtin_amdgcn_readfirstlane(kend > 0 ? (kend + BK - 1) / BK : 0);  // tiles the workgroup streams
   int wend = p.nk;
   if (CAUSAL) wend = max(0, min(wend, q0 + 32 + p.coff));
   const int wkt = q0 < p.nq ? (wend + BK - 1) / BK : 0;  // tiles with work for this wave
@@ -420,10 +421,9 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
     // place as the initial values of the four score accumulators:
     // -L / scale, -dD / scale, -D, -(D dD + B).
     constexpr int kStatLoads = 2;
-    auto issue_stats = [&](int i) {
-      const int qt = i / grp, gi = i - qt * grp;
-      const int q = min((qt_begin + qt) * BQ + n, p.nq - 1);
-      const long sb = sbase + (long)gi * p.nq;
+    auto issue_stats = [&](int i, GroupCursor c) {
+      const int q = min((qt_begin + c.qt) * BQ + n, p.nq - 1);
+      const long sb = sbase + (long)c.gi * p.nq;
       const uint32_t dst = lds_base_u32(s_q) + (uint32_t)((i % NST) * kStage + 3 * kTile);
       dma4((g ? p.delta : p.lse) + sb + q, dst);
       dma4((g ? p.bstat : p.ddelta) + sb + q, dst + 256);
@@ -450,16 +450,15 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
       }
       wait_vmem_le<0>();
     };
-    auto issue = [&](int i) {
+    auto issue = [&](int i, GroupCursor c) {
       if (wave == 3) {
-        issue_stats(i);
+        issue_stats(i, c);
         return;
       }
-      const int qt = i / grp, gi = i - qt * grp;
-      const int q0t = (qt_begin + qt) * BQ;
+      const int q0t = (qt_begin + c.qt) * BQ;
       const int nvalid = p.nq - q0t;
       const uint32_t dst = lds_wave + (uint32_t)((i % NST) * kStage);
-      const T* gsrc = src + (long)gi * D + (long)q0t * rs;
+      const T* gsrc = src + (long)c.gi * D + (long)q0t * rs;
       if (nvalid >= BQ) {
         dma.issue(dst, gsrc);
       } else {
@@ -468,19 +467,27 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
         part.issue(dst, gsrc);
       }
     };
+    GroupCursor nxt;  // iteration of the next tile to issue
 #pragma unroll
     for (int i = 0; i < NST - 1; ++i)
-      if (i < total) issue(i);
+      if (i < total) {
+        issue(i, nxt);
+        nxt.next(grp);
+      }
     if (wave == 3) {
       wait_stats(0);
       finish_stats(0);
     }
 
-    for (int i = 0; i < total; ++i) {
+    GroupCursor cur;  // iteration i
+    for (int i = 0; i < total; ++i, cur.next(grp)) {
       if (wave < 3) wait_tile<NST, G::kLoads>(i, total);
       __syncthreads();
-      if (i + NST - 1 < total) issue(i + NST - 1);
-      const int q0 = (qt_begin + i / grp) * BQ;
+      if (i + NST - 1 < total) {
+        issue(i + NST - 1, nxt);
+        nxt.next(grp);
+      }
+      const int q0 = (qt_begin + cur.qt) * BQ;
       const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
       if (active) {
         const char* st = s_q + (i % NST) * kStage;

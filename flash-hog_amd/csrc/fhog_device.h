@@ -323,6 +323,19 @@ __device__ __forceinline__ void wait_tile(int it, int total) {
   wait_vmem_le<0>();
 }
 
+// Position of an iteration of a key-tiled sweep over a group of query heads:
+// query tile qt (relative to the first) of head gi of the group, heads
+// innermost. Advanced one iteration at a time, so no division by the group size.
+struct GroupCursor {
+  int qt = 0, gi = 0;
+  __device__ __forceinline__ void next(int grp) {
+    if (++gi == grp) {
+      gi = 0;
+      ++qt;
+    }
+  }
+};
+
 // Wave-uniform LDS byte address of p (the M0 operand of the LDS DMAs).
 __device__ __forceinline__ uint32_t lds_base_u32(const void* p) {
   return __builtin_amdgcn_readfirstlane(lds_addr(p));

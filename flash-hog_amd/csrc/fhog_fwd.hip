@@ -73,8 +73,9 @@ fwd_kernel(FwdParams<T> p) {
   // Keys [0, kend) are visible to some query of the workgroup, [0, wend) to
   // some query of this wave.
   int kend = p.nk;
-  if (CAUSAL) kend = max(0, min(kend, qb * BQ + BQ + p.coff));
-  const int nkt = (kend + BK - 1) / BK;
+  if (CAUSAL) kend = min(kend, qb * BQ + BQ + p.coff);
+  // (uniform; saying so keeps the compiler from treating the loop as divergent)
+  const int nkt = __builtin_amdgcn_readfirstlane(kend > 0 ? (kend + BK - 1) / BK : 0);
   int wend = p.nk;
   if (CAUSAL) wend = max(0, min(wend, q0 + 32 + p.coff));
   const int wkt = q0 < p.nq ? (wend + BK - 1) / BK : 0;
