@@ -107,7 +107,8 @@ bwd_q_kernel(BwdParams<T> p) {
   const uint32_t row_bytes = (uint32_t)(rsk * (long)sizeof(T));
   TileDma<T, D, kPer> dma;
   dma.init(row_bytes, BK, lane, kPer * (wave & 1));
-  const uint32_t lds_tensor = lds_base_u32(s_kv) + tensor * kTile;
+  const uint32_t lds_kv = lds_base_u32(s_kv);
+  const uint32_t lds_tensor = lds_kv + tensor * kTile;
   auto issue = [&](int kt) {
     const int nvalid = p.nk - kt * BK;
     const uint32_t dst = lds_tensor + (uint32_t)((kt % NST) * kStage);
@@ -132,12 +133,12 @@ bwd_q_kernel(BwdParams<T> p) {
     __syncthreads();
     if (kt + NST - 1 < nkt) issue(kt + NST - 1);
     if (kt < wkt) {
-      const char* st = s_kv + (kt % NST) * kStage;
+      const uint32_t sa = lds_kv + (uint32_t)((kt % NST) * kStage);  // K at 0, V at kTile
       f32x16 S = zero16(), dP = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        S = mma<T>(fr.rowf(st, ks), qf[ks], S);
-        dP = mma<T>(fr.rowf(st + kTile, ks), dof[ks], dP);
+        S = mma<T>(fr.rowf(sa, 0, ks), qf[ks], S);
+        dP = mma<T>(fr.rowf(sa, kTile, ks), dof[ks], dP);
       }
       f32x16 P;
 #pragma unroll
@@ -156,7 +157,7 @@ bwd_q_kernel(BwdParams<T> p) {
         for (int e = 0; e < 8; ++e) vdS[e] = P[8 * s + e] * (dP[8 * s + e] - Di);  // dS / scale
         const V8<T> oS = cvt8<T>(vdS);
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] = mma<T>(fr.trf(st, dt, s), oS, acc[dt]);
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = mma<T>(fr.trf(sa, 0, dt, s), oS, acc[dt]);
       }
     }
   }
@@ -307,6 +308,7 @@ bwd_k_kernel(BwdParams<T> p) {
       const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
       if (active) {
         const char* st = s_q + (i % NST) * kStage;
+        const uint32_t sa = lds0 + (uint32_t)((i % NST) * kStage);  // Q at 0, dO at kTile
         const float* sc = reinterpret_cast<const float*>(st + 2 * kTile);
         // S' = S_raw - L / scale, u = dP - D (register r holds query
         // 8 (r / 4) + 4 g + r % 4 of the tile)
@@ -324,8 +326,8 @@ bwd_k_kernel(BwdParams<T> p) {
         }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          S = mma<T>(fr.rowf(st, ks), kf[ks], S);
-          dP = mma<T>(fr.rowf(st + kTile, ks), vf[ks], dP);
+          S = mma<T>(fr.rowf(sa, 0, ks), kf[ks], S);
+          dP = mma<T>(fr.rowf(sa, kTile, ks), vf[ks], dP);
         }
         f32x16 P;
 #pragma unroll
@@ -348,8 +350,8 @@ bwd_k_kernel(BwdParams<T> p) {
           const V8<T> oS = cvt8<T>(vdS);
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
-            acc_dv[dt] = mma<T>(fr.trf(st + kTile, dt, s), oP, acc_dv[dt]);
-            acc_dk[dt] = mma<T>(fr.trf(st, dt, s), oS, acc_dk[dt]);
+            acc_dv[dt] = mma<T>(fr.trf(sa, kTile, dt, s), oP, acc_dv[dt]);
+            acc_dk[dt] = mma<T>(fr.trf(sa, 0, dt, s), oS, acc_dk[dt]);
           }
         }
       }

@@ -145,7 +145,8 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   const uint32_t row_bytes = (uint32_t)(rsk * (long)sizeof(T));
   TileDma<T, D> dma;
   dma.init(row_bytes, BK, lane);
-  const uint32_t lds_wave = lds_base_u32(s_kv) + wave * kTile;
+  const uint32_t lds_kv = lds_base_u32(s_kv);
+  const uint32_t lds_wave = lds_kv + wave * kTile;
   const int total = 2 * nkt;
   // Retire the query-side loads here: otherwise the compiler waits for them at
   // their first use inside the loop, and that wait (vmcnt counts every vector
@@ -196,19 +197,16 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   for (int it = 0; it < nkt; ++it) {
     advance(it);
     if (it < wkt) {
-      const char* st = s_kv + (it % NST) * kStage;
-      const char* sK = st;
-      const char* sV = st + kTile;
-      const char* sdK = st + 2 * kTile;
-      const char* sdV = st + 3 * kTile;
+      // stage tiles at sa + 0 (K), kTile (V), 2 kTile (ddK), 3 kTile (ddV)
+      const uint32_t sa = lds_kv + (uint32_t)((it % NST) * kStage);
       f32x16 S = zero16(), ddS = zero16(), dP = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const V8<T> kf = fr.rowf(sK, ks);
+        const V8<T> kf = fr.rowf(sa, 0, ks);
         S = mma<T>(kf, qf[ks], S);
         ddS = mma<T>(kf, ddqf[ks], ddS);
-        ddS = mma<T>(fr.rowf(sdK, ks), qf[ks], ddS);
-        dP = mma<T>(fr.rowf(sV, ks), dof[ks], dP);
+        ddS = mma<T>(fr.rowf(sa, 2 * kTile, ks), qf[ks], ddS);
+        dP = mma<T>(fr.rowf(sa, kTile, ks), dof[ks], dP);
       }
       f32x16 P;
 #pragma unroll
@@ -225,7 +223,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
       for (int s = 0; s < 2; ++s) {
         const V8<T> oP = cvt8<T>(s ? hi8(P) : lo8(P));
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc_ddo[dt] = mma<T>(fr.trf(sdV, dt, s), oP, acc_ddo[dt]);
+        for (int dt = 0; dt < DT; ++dt) acc_ddo[dt] = mma<T>(fr.trf(sa, 3 * kTile, dt, s), oP, acc_ddo[dt]);
       }
     }
   }
@@ -261,21 +259,18 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
     advance(it);
     const int kt = it - nkt;
     if (kt < wkt) {
-      const char* st = s_kv + (it % NST) * kStage;
-      const char* sK = st;
-      const char* sV = st + kTile;
-      const char* sdK = st + 2 * kTile;
-      const char* sdV = st + 3 * kTile;
+      // stage tiles at sa + 0 (K), kTile (V), 2 kTile (ddK), 3 kTile (ddV)
+      const uint32_t sa = lds_kv + (uint32_t)((it % NST) * kStage);
       f32x16 S = zero16(), ddS = zero16(), dP = zero16(), dPa = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const V8<T> kf = fr.rowf(sK, ks);
+        const V8<T> kf = fr.rowf(sa, 0, ks);
         S = mma<T>(kf, qf[ks], S);
         ddS = mma<T>(kf, ddqf[ks], ddS);
-        ddS = mma<T>(fr.rowf(sdK, ks), qf[ks], ddS);
-        const V8<T> vf = fr.rowf(sV, ks);
+        ddS = mma<T>(fr.rowf(sa, 2 * kTile, ks), qf[ks], ddS);
+        const V8<T> vf = fr.rowf(sa, kTile, ks);
         dP = mma<T>(vf, dof[ks], dP);
-        dPa = mma<T>(fr.rowf(sdV, ks), dof[ks], dPa);
+        dPa = mma<T>(fr.rowf(sa, 3 * kTile, ks), dof[ks], dPa);
       }
       f32x16 P;
 #pragma unroll
@@ -300,9 +295,9 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
         const V8<T> odP = cvt8<T>(vddP);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          acc_dq2[dt] = mma<T>(fr.trf(sdK, dt, s), oS, acc_dq2[dt]);
-          acc_dq2[dt] = mma<T>(fr.trf(sK, dt, s), oS2, acc_dq2[dt]);
-          acc_ddo[dt] = mma<T>(fr.trf(sV, dt, s), odP, acc_ddo[dt]);
+          acc_dq2[dt] = mma<T>(fr.trf(sa, 2 * kTile, dt, s), oS, acc_dq2[dt]);
+          acc_dq2[dt] = mma<T>(fr.trf(sa, 0, dt, s), oS2, acc_dq2[dt]);
+          acc_ddo[dt] = mma<T>(fr.trf(sa, kTile, dt, s), odP, acc_ddo[dt]);
         }
       }
     }
@@ -413,7 +408,8 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
     const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
     TileDma<T, D> dma;
     dma.init(row_bytes, BQ, lane);
-    const uint32_t lds_wave = lds_base_u32(s_q) + wave * kTile;
+    const uint32_t lds_q = lds_base_u32(s_q);
+    const uint32_t lds_wave = lds_q + wave * kTile;
 
     // Wave 3 streams the per-query statistics of each tile with two dword DMAs
     // (lanes 0-31 then 32-63: L and D, then dD and B; rows past nq repeat row
@@ -491,9 +487,7 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
       const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
       if (active) {
         const char* st = s_q + (i % NST) * kStage;
-        const char* sQ = st;
-        const char* sdO = st + kTile;
-        const char* sdQ = st + 2 * kTile;
+        const uint32_t sa = lds_q + (uint32_t)((i % NST) * kStage);  // tiles: Q, dO, ddQ
         const float* sc = reinterpret_cast<const float*>(st + 3 * kTile);
         // The accumulators start at the per-query constants (register r holds
         // query 8 (r / 4) + 4 g + r % 4 of the tile), so they end as
@@ -517,9 +511,9 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
         }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-          const V8<T> qa = fr.rowf(sQ, ks);
-          const V8<T> dqa = fr.rowf(sdQ, ks);
-          const V8<T> doa = fr.rowf(sdO, ks);
+          const V8<T> qa = fr.rowf(sa, 0, ks);
+          const V8<T> dqa = fr.rowf(sa, 2 * kTile, ks);
+          const V8<T> doa = fr.rowf(sa, kTile, ks);
           S = mma<T>(qa, kf[ks], S);
           ddS = mma<T>(dqa, kf[ks], ddS);
           ddS = mma<T>(qa, dkf[ks], ddS);
@@ -556,9 +550,9 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
           const V8<T> odP = cvt8<T>(vddP);
 #pragma unroll
           for (int dt = 0; dt < DT; ++dt) {
-            acc_dk2[dt] = mma<T>(fr.trf(sdQ, dt, s), oS, acc_dk2[dt]);
-            acc_dk2[dt] = mma<T>(fr.trf(sQ, dt, s), oS2, acc_dk2[dt]);
-            acc_dv2[dt] = mma<T>(fr.trf(sdO, dt, s), odP, acc_dv2[dt]);
+            acc_dk2[dt] = mma<T>(fr.trf(sa, 2 * kTile, dt, s), oS, acc_dk2[dt]);
+            acc_dk2[dt] = mma<T>(fr.trf(sa, 0, dt, s), oS2, acc_dk2[dt]);
+            acc_dv2[dt] = mma<T>(fr.trf(sa, kTile, dt, s), odP, acc_dv2[dt]);
           }
         }
       }

@@ -91,93 +91,6 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float xgroup_sum(float x) { return x + __shfl_xor(x, 32, 64); }
 __device__ __forceinline__ float xgroup_max(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
 
-// ---------------------------------------------------------------------------
-// Tiles of 32 rows x D columns staged through LDS.
-//
-// A wave moves one such tile: lane (kq = l / 8, c = l % 8) owns rows 4kq..4kq+3
-// and the 8-column chunk c (plus 8 * pass for D > 64). LDS holds the tile twice:
-// row-major with a padded stride RS (for operands that contract over columns),
-// and transposed (column-major) with a padded stride TS (for operands that
-// contract over rows).
-// ---------------------------------------------------------------------------
-// Padding: a row-major row is D + 8 elements, so consecutive rows start 4
-// banks apart for 2-byte types (8 lanes of a 16-byte read are conflict free);
-// a transposed row is 36 elements, so the 8-byte (16-byte for fp32) reads of
-// 16 consecutive columns land on distinct banks.
-template <typename T, int D> struct TileGeom {
-  static constexpr int kRows = 32;
-  static constexpr int kPasses = D / 64;
-  static constexpr int RS = D + 8;
-  static constexpr int TS = kRows + 4;
-  static constexpr int kRowElems = kRows * RS;
-  static constexpr int kTrElems = D * TS;
-};
-
-template <typename T, int D> struct TileRegs {
-  V8<T> r[TileGeom<T, D>::kPasses][4];
-};
-
-// Load a 32 x D tile whose row i lives at base + i * row_stride; rows at or
-// beyond nvalid are zero-filled.
-template <typename T, int D>
-__device__ __forceinline__ void tile_load(TileRegs<T, D>& t, const T* __restrict__ base,
-                                          long row_stride, int nvalid, int lane) {
-  const int kq = lane >> 3, c = lane & 7;
-#pragma unroll
-  for (int p = 0; p < TileGeom<T, D>::kPasses; ++p) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = 4 * kq + j;
-      const int col = 8 * (c + 8 * p);
-      if (row < nvalid)
-        t.r[p][j] = *reinterpret_cast<const V8<T>*>(base + (long)row * row_stride + col);
-      else
-        t.r[p][j] = zero8<T>();
-    }
-  }
-}
-
-template <typename T, int D>
-__device__ __forceinline__ void tile_store_lds(const TileRegs<T, D>& t, T* __restrict__ row_major,
-                                               T* __restrict__ transposed, int lane) {
-  typedef TileGeom<T, D> G;
-  const int kq = lane >> 3, c = lane & 7;
-#pragma unroll
-  for (int p = 0; p < G::kPasses; ++p) {
-    const int col = 8 * (c + 8 * p);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      *reinterpret_cast<V8<T>*>(row_major + (4 * kq + j) * G::RS + col) = t.r[p][j];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      V4<T> w;
-      w[0] = t.r[p][0][e];
-      w[1] = t.r[p][1][e];
-      w[2] = t.r[p][2][e];
-      w[3] = t.r[p][3][e];
-      *reinterpret_cast<V4<T>*>(transposed + (col + e) * G::TS + 4 * kq) = w;
-    }
-  }
-}
-
-// Operand for a product contracting over columns (the head dimension): lane
-// (n, g) reads row n, columns 16 ks + 8g .. +7.
-template <typename T, int D>
-__device__ __forceinline__ V8<T> frag_row(const T* __restrict__ row_major, int n, int g, int ks) {
-  return *reinterpret_cast<const V8<T>*>(row_major + n * TileGeom<T, D>::RS + 16 * ks + 8 * g);
-}
-
-// Operand for a product contracting over the 32 tile rows, in the permuted
-// order of a C tile fed back as an operand: lane (n, g) reads column `col`,
-// rows cperm(s, g, 0..7).
-template <typename T, int D>
-__device__ __forceinline__ V8<T> frag_tr(const T* __restrict__ transposed, int col, int g, int s) {
-  const T* p = transposed + col * TileGeom<T, D>::TS + 16 * s + 4 * g;
-  V4<T> a = *reinterpret_cast<const V4<T>*>(p);
-  V4<T> b = *reinterpret_cast<const V4<T>*>(p + 8);
-  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
 // Row index (within a 32-row C tile) held by register r of a lane in group g.
 __device__ __forceinline__ int crow(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 
@@ -186,20 +99,30 @@ __device__ __forceinline__ int crow(int r, int g) { return 8 * (r >> 2) + 4 * g 
 //
 // A tile is 32 rows x D columns, stored row-major without padding; each row is
 // split into 16-byte chunks and chunk c of row r is stored at chunk position
-// c ^ swz(r) (within aligned groups of 8 chunks). swz is a permutation of 0..7
-// over any 8 consecutive rows, so the 16-byte row reads of 8 consecutive rows
-// hit 8 different bank groups; and it maps any 4 consecutive rows starting at
-// a multiple of 4 to {0,2,4,6} or {1,3,5,7}, so the 2-chunk column slices the
-// transposed reads take from 4 consecutive rows are disjoint as well.
+// c ^ swz(r) (within aligned groups of 8 chunks), swz(r) being the bit
+// reversal of (r / 2) mod 8.
+//
+// LDS serves a wave's reads in groups of lanes over 64 four-byte banks
+// (measured on gfx950: 16-byte reads in 16-lane groups, 8-byte transposed
+// reads in 32-lane groups). A 2-byte row of D = 64 is 128 bytes, half the
+// banks, so a row read (16 lanes, 16 consecutive rows, one logical chunk each)
+// is conflict free iff rows of equal parity get distinct keys, which swz gives
+// over any 16 consecutive rows starting at a multiple of 16; the transposed
+// reads (8 rows x 64 bytes per 32 lanes) are conflict free as well. With a key
+// of (r mod 8) rows r and r + 8 collide and the row reads ran at half speed
+// (278 vs 514 bytes per clock per CU).
 //
 // global_load_lds with 16 bytes per lane writes lane l's data to
 // lds_base + 16 l, so lane l of load t fills chunk position l % CH of row
 // t * (64 / CH) + l / CH and fetches the logical chunk stored there.
 // ---------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) void lds_void;
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) const char lds_cchar;
 
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+__device__ __forceinline__ int swz(int r) {
+  const int m = (r >> 1) & 7;
+  return ((m & 1) << 2) | (m & 2) | (m >> 2);
+}
 __device__ __forceinline__ int phys_chunk(int r, int c) { return (c & ~7) | ((c & 7) ^ swz(r)); }
 
 template <typename T, int D> struct SwzTile {
@@ -212,88 +135,41 @@ template <typename T, int D> struct SwzTile {
   static_assert(kChunks % 8 == 0 && kChunks <= 64, "row must be a multiple of 128 bytes");
 };
 
-// One wave-wide 16-byte-per-lane global -> LDS load: lane l's 16 bytes at
-// gptr land at lds_byte_addr + 16 l. Issued as inline assembly so that the
-// compiler does not track it: its waitcnt pass would otherwise wait for every
-// in-flight LDS DMA before each ds_read_b64_tr_b16 (it cannot prove they touch
-// different buffers), serialising the prefetch with the compute that should
-// hide it. Completion is ordered explicitly instead: wait_vmem() and a
-// workgroup barrier before a staged tile is read, a barrier before a stage is
-// overwritten. Untracked vector-memory operations only make the compiler's
-// own vmcnt waits more conservative, never less.
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_byte_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :
-               : "v"(gptr), "s"(lds_byte_addr)
-               : "memory", "m0");
-}
-
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
 
-// Issue the direct global->LDS loads of one 32 x D tile (one wave). Rows at or
-// beyond nvalid are replaced by row nvalid - 1: every consumer masks them (P = 0),
-// so they only need to hold finite data.
-template <typename T, int D>
-__device__ __forceinline__ void tile_load_lds(T* lds_tile, const T* __restrict__ rows, long row_stride,
-                                              int nvalid, int lane) {
-  typedef SwzTile<T, D> G;
-  const int p = lane % G::kChunks;
-  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds_tile));
-#pragma unroll
-  for (int t = 0; t < G::kLoads; ++t) {
-    const int row = t * G::kRowsPerLoad + lane / G::kChunks;
-    const int src_row = min(row, nvalid - 1);
-    const char* src = reinterpret_cast<const char*>(rows + (long)src_row * row_stride) + 16 * phys_chunk(row, p);
-    dma16(src, base + 1024 * t);
-  }
+// Wave-uniform LDS byte address of p (the M0 operand of the LDS DMAs).
+__device__ __forceinline__ uint32_t lds_base_u32(const void* p) {
+  return __builtin_amdgcn_readfirstlane(lds_addr(p));
 }
 
-// Operand contracting over columns: lane (n, g) gets row n, columns 16 ks + 8 g .. +7.
+// fp32 operands read from a swizzled tile (4-byte elements, 16-byte chunks of
+// 4): frag_row_swz contracts over columns (lane (n, g) gets row n, columns
+// 16 ks + 8 g .. +7), frag_tr_swz over the 32 tile rows in the permuted order
+// of a C tile fed back as an operand (lane l gets column dbase + (l & 31), rows
+// 16 s + 8 (e / 4) + 4 g + e % 4).
 template <typename T, int D>
 __device__ __forceinline__ V8<T> frag_row_swz(const T* tile, int n, int g, int ks) {
+  static_assert(sizeof(T) == 4, "2-byte types use SwzFrags' LDS reads");
   const T* row = tile + n * D;
-  if constexpr (sizeof(T) == 2) {
-    return *reinterpret_cast<const V8<T>*>(row + 8 * phys_chunk(n, 2 * ks + g));
-  } else {
-    const V4<T> a = *reinterpret_cast<const V4<T>*>(row + 4 * phys_chunk(n, 4 * ks + 2 * g));
-    const V4<T> b = *reinterpret_cast<const V4<T>*>(row + 4 * phys_chunk(n, 4 * ks + 2 * g + 1));
-    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-  }
+  const V4<T> a = *reinterpret_cast<const V4<T>*>(row + 4 * phys_chunk(n, 4 * ks + 2 * g));
+  const V4<T> b = *reinterpret_cast<const V4<T>*>(row + 4 * phys_chunk(n, 4 * ks + 2 * g + 1));
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// Operand contracting over the 32 tile rows in the permuted order of a C tile
-// fed back as an operand: lane l gets column dbase + (l & 31), rows
-// cperm(s, g, 0..7) = 16 s + 4 g + {0..3, 8..11}. For 2-byte types this is two
-// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4
-// of the 8 bytes that lane 4 e + i / 4 addresses, so lane i addresses columns
-// 4 (i % 4) .. +3 of row i / 4 of the 4-row block.
 template <typename T, int D>
 __device__ __forceinline__ V8<T> frag_tr_swz(const T* tile, int dbase, int lane, int s) {
+  static_assert(sizeof(T) == 4, "2-byte types use SwzFrags' LDS reads");
   const int g = lane >> 5;
-  if constexpr (sizeof(T) == 2) {
-    const int i = lane & 15;
-    const int d = dbase + 16 * ((lane >> 4) & 1) + 4 * (i & 3);
-    const int row = 16 * s + 4 * g + (i >> 2);
-    const int c = d >> 3, within = d & 7;
-    const T* a = tile + row * D + 8 * phys_chunk(row, c) + within;
-    const T* b = tile + (row + 8) * D + 8 * phys_chunk(row + 8, c) + within;
-    const i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a));
-    const i16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(b));
-    const V4<T> xa = __builtin_bit_cast(V4<T>, x);
-    const V4<T> yb = __builtin_bit_cast(V4<T>, y);
-    return __builtin_shufflevector(xa, yb, 0, 1, 2, 3, 4, 5, 6, 7);
-  } else {
-    const int col = dbase + (lane & 31);
-    V8<T> v;
+  const int col = dbase + (lane & 31);
+  V8<T> v;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int row = 16 * s + 8 * (e >> 2) + 4 * g + (e & 3);
-      v[e] = tile[row * D + 4 * phys_chunk(row, col >> 2) + (col & 3)];
-    }
-    return v;
+  for (int e = 0; e < 8; ++e) {
+    const int row = 16 * s + 8 * (e >> 2) + 4 * g + (e & 3);
+    v[e] = tile[row * D + 4 * phys_chunk(row, col >> 2) + (col & 3)];
   }
+  return v;
 }
 
 // Wait until this wave's outstanding vector-memory operations (including
@@ -336,15 +212,18 @@ struct GroupCursor {
   }
 };
 
-// Wave-uniform LDS byte address of p (the M0 operand of the LDS DMAs).
-__device__ __forceinline__ uint32_t lds_base_u32(const void* p) {
-  return __builtin_amdgcn_readfirstlane(lds_addr(p));
-}
+// Global -> LDS loads (LDS DMA). Each is a wave-wide global_load_lds whose
+// lane l writes its bytes to lds_byte_addr + (4 or 16) l, issued as inline
+// assembly so that the compiler does not track it: its waitcnt pass would
+// otherwise wait for every in-flight LDS DMA before each LDS read (it cannot
+// prove they touch different buffers), serialising the prefetch with the
+// compute that should hide it. Completion is ordered explicitly instead: an
+// explicit vmcnt wait and a workgroup barrier before a staged tile is read, a
+// barrier before a stage is overwritten. Untracked vector-memory operations
+// only make the compiler's own vmcnt waits more conservative, never less.
 
-// One wave-wide 16-byte-per-lane global -> LDS load addressed as a uniform
-// 64-bit base (SGPR pair) plus a per-lane 32-bit byte offset; lane l's 16 bytes
-// land at lds_byte_addr + 16 l. Untracked by the compiler for the same reason
-// as dma16.
+// 16 bytes per lane, addressed as a uniform 64-bit base (SGPR pair) plus a
+// per-lane 32-bit byte offset.
 __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
@@ -352,8 +231,7 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
                : "memory", "m0");
 }
 
-// One wave-wide 4-byte-per-lane global -> LDS load: lane l's dword at gptr
-// lands at lds_byte_addr + 4 l. Untracked by the compiler (see dma16).
+// 4 bytes per lane from a per-lane 64-bit address.
 __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_byte_addr) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                :
@@ -361,9 +239,7 @@ __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_byte_addr) {
                : "memory", "m0");
 }
 
-// One wave-wide 4-byte-per-lane global -> LDS load addressed as a uniform base
-// plus a per-lane 32-bit byte offset; lane l's dword lands at
-// lds_byte_addr + 4 l. Untracked by the compiler (see dma16).
+// 4 bytes per lane, addressed as a uniform base plus a per-lane byte offset.
 __device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
                :
@@ -371,11 +247,11 @@ __device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t
                : "memory", "m0");
 }
 
-// Per-lane source offsets of wave-wide loads that fill one swizzled 32 x D
-// tile (same placement as tile_load_lds): loads first .. first + COUNT - 1 of
-// the tile's kLoads (a wave may fill only part of a tile). They depend only on
-// the lane, the row stride and the number of valid rows, so a streaming loop
-// computes them once and then only advances the uniform base address per tile.
+// Per-lane source offsets of the wave-wide loads that fill one swizzled 32 x D
+// tile: loads first .. first + COUNT - 1 of the tile's kLoads (a wave may fill
+// only part of a tile). They depend only on the lane, the row stride and the
+// number of valid rows, so a streaming loop computes them once and then only
+// advances the uniform base address per tile.
 template <typename T, int D, int COUNT = SwzTile<T, D>::kLoads> struct TileDma {
   typedef SwzTile<T, D> G;
   static_assert(COUNT >= 1 && COUNT <= G::kLoads, "bad load count");
@@ -403,12 +279,17 @@ template <typename T, int D, int COUNT = SwzTile<T, D>::kLoads> struct TileDma {
   }
 };
 
-// Per-lane byte offsets of the MFMA operand fragments read from a swizzled
-// 32 x D tile (frag_row_swz / frag_tr_swz), computed once per kernel so that
-// each read is one address add of the tile base plus an immediate offset.
+// MFMA operand fragments read from a swizzled 32 x D tile in LDS. `stage` is
+// the wave-uniform LDS byte address of a ring stage and `off` the tile's byte
+// offset within it (a constant after inlining). For 2-byte types the per-lane
+// byte offsets are computed once per kernel, so that a read is one add of the
+// stage to a fixed per-lane offset (shared by every tile of the stage) with
+// the constant in the instruction's offset field; computing addresses from
+// pointers instead leaves the compiler to rebuild the swizzled offsets inside
+// the loop when registers are scarce.
 template <typename T, int D> struct SwzFrags {
   uint32_t row[D / 16];  // row operand of step ks
-  uint32_t tr[D / 32];   // first transposed read of column block dt, step s = 0
+  uint32_t tr[D / 32];   // first transposed read of column block dt, step 0 (rows 4 g + i / 4)
   int lane;
 
   __device__ __forceinline__ void init(int lane_id) {
@@ -419,53 +300,53 @@ template <typename T, int D> struct SwzFrags {
       for (int ks = 0; ks < D / 16; ++ks)
         row[ks] = 2u * (uint32_t)(n * D + 8 * phys_chunk(n, 2 * ks + g));
       const int i = lane & 15;
-      const int row0 = 4 * g + (i >> 2);
+      const int r = 4 * g + (i >> 2);
 #pragma unroll
       for (int dt = 0; dt < D / 32; ++dt) {
         const int d = 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (i & 3);
-        tr[dt] = 2u * (uint32_t)(row0 * D + 8 * phys_chunk(row0, d >> 3) + (d & 7));
+        tr[dt] = 2u * (uint32_t)(r * D + 8 * phys_chunk(r, d >> 3) + (d & 7));
       }
     }
   }
 
   // Operand contracting over columns: lane (n, g) gets row n, columns 16 ks + 8 g .. +7.
-  __device__ __forceinline__ V8<T> rowf(const char* tile, int ks) const {
+  __device__ __forceinline__ V8<T> rowf(uint32_t stage, int off, int ks) const {
     if constexpr (sizeof(T) == 2) {
-      return *reinterpret_cast<const V8<T>*>(tile + row[ks]);
+      const lds_cchar* p = reinterpret_cast<const lds_cchar*>((uintptr_t)(stage + row[ks]));
+      return *reinterpret_cast<const __attribute__((address_space(3))) V8<T>*>(p + off);
     } else {
-      return frag_row_swz<T, D>(reinterpret_cast<const T*>(tile), lane & 31, lane >> 5, ks);
+      return frag_row_swz<T, D>(tile_ptr(stage, off), lane & 31, lane >> 5, ks);
     }
   }
 
-  // Operand contracting over the tile rows in the permuted C order (frag_tr_swz):
-  // rows 16 s + 4 g + {0..3} and the same + 8 share the swizzle of rows 4 g + {0..3}
-  // (the swizzle repeats every 8 rows), so both reads are fixed offsets from tr[dt].
-  __device__ __forceinline__ V8<T> trf(const char* tile, int dt, int s) const {
+  // Operand contracting over the tile rows in the permuted C order: lane l gets
+  // column 32 dt + (l & 31), rows 16 s + 8 (e / 4) + 4 g + e % 4. For 2-byte
+  // types that is two ds_read_b64_tr_b16 (rows 16 s + 4 g + {0..3} and the same
+  // + 8): within each 16-lane group, lane i receives element i % 4 of the 8
+  // bytes that lane 4 e + i / 4 addresses, so lane i addresses columns
+  // 4 (i % 4) .. +3 of row i / 4 of the 4-row block. The swizzle repeats every
+  // 16 rows, so step s is a constant offset from step 0; and swz(r + 8) =
+  // swz(r) ^ 1, so the second read's address is the first one with bit 4 (the
+  // chunk's lowest bit) flipped, 8 rows further on. That needs stage + off to
+  // be a multiple of 32, which every ring stage and tile offset here is.
+  __device__ __forceinline__ V8<T> trf(uint32_t stage, int off, int dt, int s) const {
     if constexpr (sizeof(T) == 2) {
-      const char* a = tile + tr[dt] + s * 32 * D;
+      const uint32_t a0 = stage + tr[dt];
+      const lds_cchar* a = reinterpret_cast<const lds_cchar*>((uintptr_t)a0) + off + s * 32 * D;
+      const lds_cchar* b = reinterpret_cast<const lds_cchar*>((uintptr_t)(a0 ^ 16u)) + off + s * 32 * D + 16 * D;
       const i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a));
-      const i16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a + 16 * D));
-      const V4<T> xa = __builtin_bit_cast(V4<T>, x);
-      const V4<T> yb = __builtin_bit_cast(V4<T>, y);
-      return __builtin_shufflevector(xa, yb, 0, 1, 2, 3, 4, 5, 6, 7);
+      const i16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(b));
+      return __builtin_shufflevector(__builtin_bit_cast(V4<T>, x), __builtin_bit_cast(V4<T>, y), 0, 1, 2, 3, 4, 5,
+                                     6, 7);
     } else {
-      return frag_tr_swz<T, D>(reinterpret_cast<const T*>(tile), 32 * dt, lane, s);
+      return frag_tr_swz<T, D>(tile_ptr(stage, off), 32 * dt, lane, s);
     }
+  }
+
+ private:
+  __device__ __forceinline__ static const T* tile_ptr(uint32_t stage, int off) {
+    return reinterpret_cast<const T*>(reinterpret_cast<const lds_cchar*>((uintptr_t)stage) + off);
   }
 };
-
-// ---------------------------------------------------------------------------
-// Grid mapping. Workgroups are dispatched round-robin over the 8 XCDs of an
-// MI355X, each with its own L2. Blocks that read the same (batch, head) stream
-// are therefore remapped onto one XCD, in order, so that their shared K/V (or
-// Q/dO) tiles hit that XCD's L2.
-// ---------------------------------------------------------------------------
-constexpr int kNumXcd = 8;
-
-__device__ __forceinline__ int xcd_remap(int id, int total) {
-  const int per = total / kNumXcd;
-  if (id >= per * kNumXcd) return id;
-  return (id % kNumXcd) * per + id / kNumXcd;
-}
 
 }  // namespace fhog

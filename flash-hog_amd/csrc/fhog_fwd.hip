@@ -87,7 +87,8 @@ fwd_kernel(FwdParams<T> p) {
   const uint32_t row_bytes = (uint32_t)(rsk * (long)sizeof(T));
   TileDma<T, D, kPer> dma;
   dma.init(row_bytes, BK, lane, kPer * (wave & 1));
-  const uint32_t lds_tensor = lds_base_u32(s_kv) + tensor * kTile;
+  const uint32_t lds_kv = lds_base_u32(s_kv);
+  const uint32_t lds_tensor = lds_kv + tensor * kTile;
   auto issue = [&](int kt) {
     const int nvalid = p.nk - kt * BK;
     const uint32_t dst = lds_tensor + (uint32_t)((kt % NST) * kStage);
@@ -121,10 +122,10 @@ fwd_kernel(FwdParams<T> p) {
     __syncthreads();
     if (kt + NST - 1 < nkt) issue(kt + NST - 1);
     if (kt < wkt) {
-      const char* st = s_kv + (kt % NST) * kStage;
+      const uint32_t sa = lds_kv + (uint32_t)((kt % NST) * kStage);  // K at 0, V at kTile
       f32x16 S = zero16();
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) S = mma<T>(fr.rowf(st, ks), qf[ks], S);
+      for (int ks = 0; ks < KS; ++ks) S = mma<T>(fr.rowf(sa, 0, ks), qf[ks], S);
 #pragma unroll
       for (int r = 0; r < 16; ++r) S[r] *= c2;
       const int k0 = kt * BK;
@@ -156,7 +157,7 @@ fwd_kernel(FwdParams<T> p) {
       for (int s = 0; s < 2; ++s) {
         const V8<T> oP = cvt8<T>(s ? hi8(S) : lo8(S));
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] = mma<T>(fr.trf(st + kTile, dt, s), oP, acc[dt]);
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = mma<T>(fr.trf(sa, kTile, dt, s), oP, acc[dt]);
       }
     }
   }
