@@ -37,6 +37,10 @@ HIPCC_FLAGS = [
 ]
 
 
+# Extra flags for single sources (none at present).
+SOURCE_FLAGS: dict[str, list[str]] = {}
+
+
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(exe):
@@ -45,7 +49,7 @@ def hipcc() -> str:
 
 
 def _compile(src: pathlib.Path, obj: pathlib.Path) -> None:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")

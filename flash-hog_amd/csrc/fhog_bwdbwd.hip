@@ -593,8 +593,13 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stage
   const int nqb = (p.nq + 32 * kWaves - 1) / (32 * kWaves);
   const int nkb = (p.nk + 32 * kWaves - 1) / (32 * kWaves);
   if (stages & 1) {
-    hipLaunchKernelGGL((bwdbwd_q_kernel<T, D, CAUSAL>), dim3(nqb * p.batch * p.heads), dim3(kThreads), 0, stream, p);
-    hipError_t e = hipGetLastError();
+    hipError_t e;
+    if constexpr (sizeof(T) == 2 && D == 64) {
+      e = launch_bwdbwd_stage1_fused<T, D, CAUSAL>(p, stream);
+    } else {
+      hipLaunchKernelGGL((bwdbwd_q_kernel<T, D, CAUSAL>), dim3(nqb * p.batch * p.heads), dim3(kThreads), 0, stream, p);
+      e = hipGetLastError();
+    }
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {

@@ -1,0 +1,303 @@
+// Stage 1 of the Flash-HOG double backward (passes 1-3) in one sweep over the
+// keys, for 2-byte types at D = 64 (fhog_bwdbwd.hip holds the two-sweep
+// stage 1 used for the other shapes, and stage 2). The math follows
+// flash_hog/_jax_refs/jax_impl.py:273-336 and the pass split of
+// flash_hog/jax/_pallas_gpu_kernel.py:149-278; outputs and row statistics are
+// those of fhog_bwdbwd.hip's stage 1.
+//
+// One sweep. dD and B are only known at the end of the sweep, but they enter
+// dQ2 and ddO as per-row factors of sums that can be accumulated separately.
+// With u = dP - D, x = P ddS (ddS including its scale) and
+// X = P (dPa + ddS u):
+//   dQ2 = scale (sum_j P u ddK + sum_j X K - dD sum_j P u K - c sum_j P K),
+//   ddO = sum_j P ddV + sum_j x V - dD sum_j P V,       c = D dD + B,
+// because P (dP2 - B) = X - dD P u - c P and ddP = x - dD P. Every key tile is
+// streamed once; per tile a wave forms the five score products (S, ddS twice,
+// dP, dPa), one exp per pair, and seven output products into five
+// accumulators (dQ2 part, sum P u K, sum P K, ddO part, sum P V).
+//
+// Sixteen queries per wave. The five accumulators of 32 queries would not fit
+// beside the score tiles in the 256 registers of a wave that shares its SIMD
+// with another, and two co-resident waves are what overlaps one wave's matrix
+// work with the other's vector work. So a wave owns 16 queries and uses the
+// 16x16x32 matrix instruction (v_mfma_f32_16x16x32_{bf16,f16}):
+//   A (16 x 32): lane holds A[m = l % 16][k = 8 (l / 16) + e],   e = 0..7
+//   B (32 x 16): lane holds B[k = 8 (l / 16) + e][n = l % 16]
+//   C (16 x 16): lane holds C[m = 4 (l / 16) + i][n = l % 16],   i = 0..3
+// Score tiles are transposed (keys x queries, two 16-key C tiles per 32-key
+// tile), so each lane holds one query; a C tile pair fed back as the B
+// operand of an output product contracts over keys in the permuted order
+// k' = 8 g + e -> key 4 g + e (e < 4) or 16 + 4 g + e - 4 (e >= 4), and the
+// A operand (the key-side tile, transposed) is read with two
+// ds_read_b64_tr_b16 in the same order.
+#include "fhog_device.h"
+#include "fhog_params.h"
+
+namespace fhog {
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kQ = 16;  // queries per wave
+
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+template <typename T> __device__ __forceinline__ f32x4v mma16(V8<T> a, V8<T> b, f32x4v c);
+template <> __device__ __forceinline__ f32x4v mma16<__bf16>(bf16x8 a, bf16x8 b, f32x4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ f32x4v mma16<_Float16>(f16x8 a, f16x8 b, f32x4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4v zero4() { return f32x4v{0.f, 0.f, 0.f, 0.f}; }
+
+// Sum over the four 16-lane groups (lanes holding the same query).
+__device__ __forceinline__ float group4_sum(float x) {
+  x += __shfl_xor(x, 16, 64);
+  return x + __shfl_xor(x, 32, 64);
+}
+
+// Per-lane LDS byte offsets of the 16x16x32 operand fragments read from a
+// swizzled 32 x D tile (2-byte types).
+template <typename T, int D> struct SwzFrags16 {
+  static_assert(sizeof(T) == 2, "2-byte types only");
+  uint32_t row[D / 32];  // score A operand: row l % 16, columns 32 ks + 8 (l / 16) .. +7
+  uint32_t tr[D / 16];   // output A operand of column block db: rows 4 (l / 16) + i / 4
+  __device__ __forceinline__ void init(int lane) {
+    const int n = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) row[ks] = 2u * (uint32_t)(n * D + 8 * phys_chunk(n, 4 * ks + g));
+    const int r = 4 * g + (n >> 2);
+#pragma unroll
+    for (int db = 0; db < D / 16; ++db) {
+      const int d = 16 * db + 4 * (n & 3);
+      tr[db] = 2u * (uint32_t)(r * D + 8 * phys_chunk(r, d >> 3) + (d & 7));
+    }
+  }
+  // Keys 16 kb + l % 16 of the tile at stage + off, step ks. The swizzle
+  // repeats every 16 rows, so kb is a constant offset.
+  __device__ __forceinline__ V8<T> rowf(uint32_t stage, int off, int kb, int ks) const {
+    const lds_cchar* p = reinterpret_cast<const lds_cchar*>((uintptr_t)(stage + row[ks])) + off + kb * 16 * D * 2;
+    return *reinterpret_cast<const __attribute__((address_space(3))) V8<T>*>(p);
+  }
+  // Column 16 db + l % 16, keys 4 g + {0..3} and 16 + 4 g + {0..3}: within a
+  // 16-lane group, lane i addresses row 4 g + i / 4, columns 16 db + 4 (i % 4)
+  // .. +3, and receives column 16 db + i of the four rows.
+  __device__ __forceinline__ V8<T> trf(uint32_t stage, int off, int db) const {
+    const lds_cchar* a = reinterpret_cast<const lds_cchar*>((uintptr_t)(stage + tr[db])) + off;
+    const i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a));
+    const i16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a + 16 * D * 2));
+    return __builtin_shufflevector(__builtin_bit_cast(V4<T>, x), __builtin_bit_cast(V4<T>, y), 0, 1, 2, 3, 4, 5, 6,
+                                   7);
+  }
+};
+
+template <typename T, int D, bool CAUSAL>
+__global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(2, 2)))
+bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
+  typedef SwzTile<T, D> G;
+  constexpr int KS = D / 32;       // 32-deep steps over the head dim (score products)
+  constexpr int DB = D / 16;       // 16-wide output column blocks
+  constexpr int BQ = kQ * kWaves;  // queries per workgroup
+  constexpr int BK = 32;           // keys per streamed tile
+  constexpr int NST = 3;
+  constexpr int kTile = G::kElems * (int)sizeof(T);
+  constexpr int kStage = 4 * kTile;  // K, V, ddK, ddV
+  __shared__ __attribute__((aligned(1024))) char s_kv[NST * kStage];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int nqb = (p.nq + BQ - 1) / BQ;
+  const int nbh = p.batch * p.heads;
+  const int rank = blockIdx.x / nbh;
+  const int bh = blockIdx.x - rank * nbh;
+  const int qb = CAUSAL ? nqb - 1 - rank : rank;
+  const int b = bh / p.heads, h = bh % p.heads;
+  const int hk = h / (p.heads / p.kv_heads);
+  const long rs = (long)p.heads * D;      // query-side row stride
+  const long rsk = (long)p.kv_heads * D;  // key-side row stride
+  const long qbase = ((long)b * p.nq * p.heads + h) * D;
+  const long kbase = ((long)b * p.nk * p.kv_heads + hk) * D;
+  const long sbase = (long)bh * p.nq;
+  const int q0 = qb * BQ + wave * kQ;
+  const int qi = q0 + n;
+  const bool qvalid = qi < p.nq;
+
+  // Query-side operands (B of the score products) and D_i = <O_i, dO_i>.
+  V8<T> qf[KS], ddqf[KS], dof[KS];
+  float dpart = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const long off = qbase + (long)qi * rs + 32 * ks + 8 * g;
+    if (qvalid) {
+      qf[ks] = *reinterpret_cast<const V8<T>*>(p.q + off);
+      ddqf[ks] = *reinterpret_cast<const V8<T>*>(p.ddq + off);
+      dof[ks] = *reinterpret_cast<const V8<T>*>(p.dout + off);
+      const V8<T> of = *reinterpret_cast<const V8<T>*>(p.o + off);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dpart += (float)of[e] * (float)dof[ks][e];
+    } else {
+      qf[ks] = zero8<T>();
+      ddqf[ks] = zero8<T>();
+      dof[ks] = zero8<T>();
+    }
+  }
+  const float scale = p.scale;
+  const float c2 = scale * kLog2e;
+  const float Di = group4_sum(dpart);
+  const float nD = -Di;
+  const float nL2 = qvalid ? -p.lse[sbase + qi] * kLog2e : 0.f;
+
+  // Keys [0, kend) are visible to some query of the workgroup, [0, wend) to
+  // some query of this wave.
+  int kend = p.nk;
+  if (CAUSAL) kend = min(kend, qb * BQ + BQ + p.coff);
+  // (uniform; saying so keeps the compiler from treating the loop as divergent)
+  const int nkt = __builtin_amdgcn_readfirstlane(kend > 0 ? (kend + BK - 1) / BK : 0);
+  int wend = p.nk;
+  if (CAUSAL) wend = max(0, min(wend, q0 + kQ + p.coff));
+  const int wkt = q0 < p.nq ? (wend + BK - 1) / BK : 0;  // tiles with work for this wave
+
+  SwzFrags16<T, D> fr;
+  fr.init(lane);
+
+  // Wave w streams key-side tensor w (K, V, ddK, ddV) into an NST-stage ring.
+  const T* src = (wave == 0 ? p.k : wave == 1 ? p.v : wave == 2 ? p.ddk : p.ddv) + kbase;
+  const uint32_t row_bytes = (uint32_t)(rsk * (long)sizeof(T));
+  TileDma<T, D> dma;
+  dma.init(row_bytes, BK, lane);
+  const uint32_t lds_kv = lds_base_u32(s_kv);
+  const uint32_t lds_wave = lds_kv + wave * kTile;
+  // Retire the query-side loads before the ring starts: vmcnt counts the
+  // untracked LDS DMAs too, so a wait for them inside the loop would drain the
+  // prefetched tiles.
+  wait_vmem();
+  auto issue = [&](int kt) {
+    const int nvalid = p.nk - kt * BK;
+    const uint32_t dst = lds_wave + (uint32_t)((kt % NST) * kStage);
+    const T* gsrc = src + (long)kt * BK * rsk;
+    if (nvalid >= BK) {
+      dma.issue(dst, gsrc);
+    } else {
+      TileDma<T, D> part;
+      part.init(row_bytes, nvalid, lane);
+      part.issue(dst, gsrc);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < NST - 1; ++i)
+    if (i < nkt) issue(i);
+
+  f32x4v acc_a[DB], acc_s[DB], acc_p[DB], acc_o[DB], acc_pv[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc_a[db] = acc_s[db] = acc_p[db] = acc_o[db] = acc_pv[db] = zero4();
+  float dd_acc = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+
+  for (int kt = 0; kt < nkt; ++kt) {
+    wait_tile<NST, G::kLoads>(kt, nkt);
+    __syncthreads();
+    if (kt + NST - 1 < nkt) issue(kt + NST - 1);
+    if (kt < wkt) {
+      // stage tiles at sa + 0 (K), kTile (V), 2 kTile (ddK), 3 kTile (ddV)
+      const uint32_t sa = lds_kv + (uint32_t)((kt % NST) * kStage);
+      f32x4v S[2], ddS[2], dP[2], dPa[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        S[kb] = ddS[kb] = dP[kb] = dPa[kb] = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const V8<T> kf = fr.rowf(sa, 0, kb, ks);
+          S[kb] = mma16<T>(kf, qf[ks], S[kb]);
+          ddS[kb] = mma16<T>(kf, ddqf[ks], ddS[kb]);
+          ddS[kb] = mma16<T>(fr.rowf(sa, 2 * kTile, kb, ks), qf[ks], ddS[kb]);
+          dP[kb] = mma16<T>(fr.rowf(sa, kTile, kb, ks), dof[ks], dP[kb]);
+          dPa[kb] = mma16<T>(fr.rowf(sa, 3 * kTile, kb, ks), dof[ks], dPa[kb]);
+        }
+      }
+      // Element e of the permuted key order: C tile e / 4, register e % 4
+      // (tile-relative key 16 (e / 4) + 4 g + e % 4).
+      const int k0 = kt * BK;
+      const bool need_mask = (k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0 + p.coff);
+      const int klim = min(p.nk - 1, CAUSAL ? qi + p.coff : p.nk - 1) - k0;  // last visible key, tile-relative
+      f32x8 vP, vx, vu, vX;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int kb = e >> 2, i = e & 3;
+        float P = exp2_fast(fmaf(S[kb][i], c2, nL2));
+        if (need_mask && 16 * kb + 4 * g + i > klim) P = 0.f;
+        const float x = P * (ddS[kb][i] * scale);  // P ddS
+        const float u = dP[kb][i] + nD;            // dP - D
+        const float pa = P * dPa[kb][i];
+        dd_acc += x;
+        r1 += pa;
+        r2 = fmaf(dP[kb][i], P, r2);
+        r3 = fmaf(dP[kb][i], x, r3);
+        vP[e] = P;
+        vx[e] = x;
+        vu[e] = P * u;           // P u
+        vX[e] = fmaf(x, u, pa);  // P (dPa + ddS u)
+      }
+      const V8<T> oP = cvt8<T>(vP), ox = cvt8<T>(vx), ou = cvt8<T>(vu), oX = cvt8<T>(vX);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const V8<T> tK = fr.trf(sa, 0, db);
+        const V8<T> tV = fr.trf(sa, kTile, db);
+        acc_a[db] = mma16<T>(fr.trf(sa, 2 * kTile, db), ou, acc_a[db]);
+        acc_a[db] = mma16<T>(tK, oX, acc_a[db]);
+        acc_s[db] = mma16<T>(tK, ou, acc_s[db]);
+        acc_p[db] = mma16<T>(tK, oP, acc_p[db]);
+        acc_o[db] = mma16<T>(fr.trf(sa, 3 * kTile, db), oP, acc_o[db]);
+        acc_o[db] = mma16<T>(tV, ox, acc_o[db]);
+        acc_pv[db] = mma16<T>(tV, oP, acc_pv[db]);
+      }
+    }
+  }
+
+  const float dD = group4_sum(dd_acc);
+  const float Bi = group4_sum(r1) - dD * group4_sum(r2) - Di * dD + group4_sum(r3);
+  const float c = fmaf(Di, dD, Bi);
+  if (qvalid) {
+    if (g == 0) {
+      p.delta[sbase + qi] = Di;
+      p.ddelta[sbase + qi] = dD;
+      p.bstat[sbase + qi] = Bi;
+    }
+    T* dq2 = p.dq2 + qbase + (long)qi * rs;
+    T* ddo = p.ddo + qbase + (long)qi * rs;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int d = 16 * db + 4 * g;  // this lane's four output columns
+      f32x4 x, y;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] = scale * (acc_a[db][i] - dD * acc_s[db][i] - c * acc_p[db][i]);
+        y[i] = acc_o[db][i] - dD * acc_pv[db][i];
+      }
+      *reinterpret_cast<V4<T>*>(dq2 + d) = cvt4<T>(x);
+      *reinterpret_cast<V4<T>*>(ddo + d) = cvt4<T>(y);
+    }
+  }
+}
+
+}  // namespace
+
+template <typename T, int D, bool CAUSAL>
+hipError_t launch_bwdbwd_stage1_fused(const BwdBwdParams<T>& p, hipStream_t stream) {
+  const int nqb = (p.nq + kQ * kWaves - 1) / (kQ * kWaves);
+  hipLaunchKernelGGL((bwdbwd_q_fused_kernel<T, D, CAUSAL>), dim3(nqb * p.batch * p.heads), dim3(kThreads), 0, stream,
+                     p);
+  return hipGetLastError();
+}
+
+#define FHOG_INST(T, C) template hipError_t launch_bwdbwd_stage1_fused<T, 64, C>(const BwdBwdParams<T>&, hipStream_t);
+FHOG_INST(__bf16, true)
+FHOG_INST(__bf16, false)
+FHOG_INST(_Float16, true)
+FHOG_INST(_Float16, false)
+#undef FHOG_INST
+
+}  // namespace fhog

@@ -345,7 +345,8 @@ template <typename T, int D> struct SwzFrags {
 
  private:
   __device__ __forceinline__ static const T* tile_ptr(uint32_t stage, int off) {
-    return reinterpret_cast<const T*>(reinterpret_cast<const lds_cchar*>((uintptr_t)stage) + off);
+    // an address-space conversion, which only a C-style cast expresses
+    return (const T*)((const lds_cchar*)(uintptr_t)stage + off);
   }
 };
 
