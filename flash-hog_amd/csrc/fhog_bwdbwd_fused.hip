@@ -30,6 +30,8 @@
 // k' = 8 g + e -> key 4 g + e (e < 4) or 16 + 4 g + e - 4 (e >= 4), and the
 // A operand (the key-side tile, transposed) is read with two
 // ds_read_b64_tr_b16 in the same order.
+#include <type_traits>
+
 #include "fhog_device.h"
 #include "fhog_params.h"
 
@@ -52,6 +54,12 @@ template <> __device__ __forceinline__ f32x4v mma16<_Float16>(f16x8 a, f16x8 b, 
 }
 
 __device__ __forceinline__ f32x4v zero4() { return f32x4v{0.f, 0.f, 0.f, 0.f}; }
+
+// The four score tiles of a 32-key tile for one wave (two 16-key C tiles
+// each), transposed (keys x queries): S, ddS (without its scale), dP, dPa.
+struct Scores {
+  f32x4v S[2], ddS[2], dP[2], dPa[2];
+};
 
 // Sum over the four 16-lane groups (lanes holding the same query).
 __device__ __forceinline__ float group4_sum(float x) {
@@ -103,7 +111,7 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
   constexpr int DB = D / 16;       // 16-wide output column blocks
   constexpr int BQ = kQ * kWaves;  // queries per workgroup
   constexpr int BK = 32;           // keys per streamed tile
-  constexpr int NST = 3;
+  constexpr int NST = 4;  // tiles t (finishing), t + 1 (scores), two in flight
   constexpr int kTile = G::kElems * (int)sizeof(T);
   constexpr int kStage = 4 * kTile;  // K, V, ddK, ddV
   __shared__ __attribute__((aligned(1024))) char s_kv[NST * kStage];
@@ -188,72 +196,128 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
       part.issue(dst, gsrc);
     }
   };
+  int hi = -1;  // last tile issued
 #pragma unroll
   for (int i = 0; i < NST - 1; ++i)
-    if (i < nkt) issue(i);
+    if (i < nkt) issue(++hi);
 
   f32x4v acc_a[DB], acc_s[DB], acc_p[DB], acc_o[DB], acc_pv[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc_a[db] = acc_s[db] = acc_p[db] = acc_o[db] = acc_pv[db] = zero4();
   float dd_acc = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
 
-  for (int kt = 0; kt < nkt; ++kt) {
-    wait_tile<NST, G::kLoads>(kt, nkt);
+  // Score tiles of the key tile in slot sa (K at 0, V at kTile, ddK at
+  // 2 kTile, ddV at 3 kTile); kb = 16-key half.
+  auto scores = [&](uint32_t sa, Scores& sc) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sc.S[kb] = sc.ddS[kb] = sc.dP[kb] = sc.dPa[kb] = zero4();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const V8<T> kf = fr.rowf(sa, 0, kb, ks);
+        sc.S[kb] = mma16<T>(kf, qf[ks], sc.S[kb]);
+        sc.ddS[kb] = mma16<T>(kf, ddqf[ks], sc.ddS[kb]);
+        sc.ddS[kb] = mma16<T>(fr.rowf(sa, 2 * kTile, kb, ks), qf[ks], sc.ddS[kb]);
+        sc.dP[kb] = mma16<T>(fr.rowf(sa, kTile, kb, ks), dof[ks], sc.dP[kb]);
+        sc.dPa[kb] = mma16<T>(fr.rowf(sa, 3 * kTile, kb, ks), dof[ks], sc.dPa[kb]);
+      }
+    }
+  };
+  // Element-wise step and output products of the key tile in slot sa whose
+  // scores are sc. Element e of the permuted key order is C tile e / 4,
+  // register e % 4 (tile-relative key 16 (e / 4) + 4 g + e % 4); keys past
+  // klim are masked when MASK.
+  auto finish = [&](uint32_t sa, const Scores& sc, int klim, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    f32x8 vP, vx, vu, vX;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int kb = e >> 2, i = e & 3;
+      float P = exp2_fast(fmaf(sc.S[kb][i], c2, nL2));
+      if (MASK && 16 * kb + 4 * g + i > klim) P = 0.f;
+      const float x = P * (sc.ddS[kb][i] * scale);  // P ddS
+      const float u = sc.dP[kb][i] + nD;            // dP - D
+      const float pa = P * sc.dPa[kb][i];
+      dd_acc += x;
+      r1 += pa;
+      r2 = fmaf(sc.dP[kb][i], P, r2);
+      r3 = fmaf(sc.dP[kb][i], x, r3);
+      vP[e] = P;
+      vx[e] = x;
+      vu[e] = P * u;           // P u
+      vX[e] = fmaf(x, u, pa);  // P (dPa + ddS u)
+    }
+    const V8<T> oP = cvt8<T>(vP), ox = cvt8<T>(vx), ou = cvt8<T>(vu), oX = cvt8<T>(vX);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const V8<T> tK = fr.trf(sa, 0, db);
+      const V8<T> tV = fr.trf(sa, kTile, db);
+      acc_a[db] = mma16<T>(fr.trf(sa, 2 * kTile, db), ou, acc_a[db]);
+      acc_a[db] = mma16<T>(tK, oX, acc_a[db]);
+      acc_s[db] = mma16<T>(tK, ou, acc_s[db]);
+      acc_p[db] = mma16<T>(tK, oP, acc_p[db]);
+      acc_o[db] = mma16<T>(fr.trf(sa, 3 * kTile, db), oP, acc_o[db]);
+      acc_o[db] = mma16<T>(tV, ox, acc_o[db]);
+      acc_pv[db] = mma16<T>(tV, oP, acc_pv[db]);
+    }
+  };
+  auto slot = [&](int kt) { return lds_kv + (uint32_t)((kt % NST) * kStage); };
+  // Waits for tile `need` and makes every wave's copy visible; `hi` is the last
+  // tile issued (tiles after `need`, at most NST - 2, may still be in flight).
+  auto advance = [&](int need) {
+    const int ahead = hi - need;
+    if (ahead >= 2)
+      wait_vmem_le<2 * G::kLoads>();
+    else if (ahead == 1)
+      wait_vmem_le<G::kLoads>();
+    else
+      wait_vmem_le<0>();
     __syncthreads();
-    if (kt + NST - 1 < nkt) issue(kt + NST - 1);
-    if (kt < wkt) {
-      // stage tiles at sa + 0 (K), kTile (V), 2 kTile (ddK), 3 kTile (ddV)
-      const uint32_t sa = lds_kv + (uint32_t)((kt % NST) * kStage);
-      f32x4v S[2], ddS[2], dP[2], dPa[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        S[kb] = ddS[kb] = dP[kb] = dPa[kb] = zero4();
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const V8<T> kf = fr.rowf(sa, 0, kb, ks);
-          S[kb] = mma16<T>(kf, qf[ks], S[kb]);
-          ddS[kb] = mma16<T>(kf, ddqf[ks], ddS[kb]);
-          ddS[kb] = mma16<T>(fr.rowf(sa, 2 * kTile, kb, ks), qf[ks], ddS[kb]);
-          dP[kb] = mma16<T>(fr.rowf(sa, kTile, kb, ks), dof[ks], dP[kb]);
-          dPa[kb] = mma16<T>(fr.rowf(sa, 3 * kTile, kb, ks), dof[ks], dPa[kb]);
-        }
-      }
-      // Element e of the permuted key order: C tile e / 4, register e % 4
-      // (tile-relative key 16 (e / 4) + 4 g + e % 4).
-      const int k0 = kt * BK;
-      const bool need_mask = (k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0 + p.coff);
-      const int klim = min(p.nk - 1, CAUSAL ? qi + p.coff : p.nk - 1) - k0;  // last visible key, tile-relative
-      f32x8 vP, vx, vu, vX;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int kb = e >> 2, i = e & 3;
-        float P = exp2_fast(fmaf(S[kb][i], c2, nL2));
-        if (need_mask && 16 * kb + 4 * g + i > klim) P = 0.f;
-        const float x = P * (ddS[kb][i] * scale);  // P ddS
-        const float u = dP[kb][i] + nD;            // dP - D
-        const float pa = P * dPa[kb][i];
-        dd_acc += x;
-        r1 += pa;
-        r2 = fmaf(dP[kb][i], P, r2);
-        r3 = fmaf(dP[kb][i], x, r3);
-        vP[e] = P;
-        vx[e] = x;
-        vu[e] = P * u;           // P u
-        vX[e] = fmaf(x, u, pa);  // P (dPa + ddS u)
-      }
-      const V8<T> oP = cvt8<T>(vP), ox = cvt8<T>(vx), ou = cvt8<T>(vu), oX = cvt8<T>(vX);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const V8<T> tK = fr.trf(sa, 0, db);
-        const V8<T> tV = fr.trf(sa, kTile, db);
-        acc_a[db] = mma16<T>(fr.trf(sa, 2 * kTile, db), ou, acc_a[db]);
-        acc_a[db] = mma16<T>(tK, oX, acc_a[db]);
-        acc_s[db] = mma16<T>(tK, ou, acc_s[db]);
-        acc_p[db] = mma16<T>(tK, oP, acc_p[db]);
-        acc_o[db] = mma16<T>(fr.trf(sa, 3 * kTile, db), oP, acc_o[db]);
-        acc_o[db] = mma16<T>(tV, ox, acc_o[db]);
-        acc_pv[db] = mma16<T>(tV, oP, acc_pv[db]);
-      }
+  };
+
+  // Full tiles [0, nfull): visible to every query of the workgroup and inside
+  // nk, so no mask. Pipelined: the scores of tile t + 1 are formed in the step
+  // that finishes tile t, so each wave has independent matrix work to issue
+  // beside its element-wise work. Buffers alternate, the loop being unrolled
+  // by two.
+  int full = p.nk / BK;
+  if (CAUSAL) full = min(full, max(0, qb * BQ + p.coff + 1) / BK);
+  const int nfull = __builtin_amdgcn_readfirstlane(min(full, nkt));
+  auto step = [&](int t, Scores& cur, Scores& nxt, auto next_tag) {
+    constexpr bool NEXT = decltype(next_tag)::value;
+    advance(NEXT ? t + 1 : t);
+    if (hi + 1 < nkt) issue(++hi);
+    if constexpr (NEXT) scores(slot(t + 1), nxt);
+    finish(slot(t), cur, 0, std::false_type{});
+  };
+
+  int t = 0;
+  if (nfull > 0) {
+    Scores A, B;
+    advance(0);
+    scores(slot(0), A);
+    for (; t + 2 < nfull; t += 2) {
+      step(t, A, B, std::true_type{});
+      step(t + 1, B, A, std::true_type{});
+    }
+    if (t + 1 < nfull) {
+      step(t, A, B, std::true_type{});
+      step(t + 1, B, A, std::false_type{});
+      t += 2;
+    } else {
+      step(t, A, B, std::false_type{});
+      t += 1;
+    }
+  }
+  // Diagonal and ragged tiles, one per step, masked; only waves with work.
+  for (; t < nkt; ++t) {
+    advance(t);
+    if (hi + 1 < nkt) issue(++hi);
+    if (t < wkt) {
+      Scores sc;
+      scores(slot(t), sc);
+      const int klim = min(p.nk - 1, CAUSAL ? qi + p.coff : p.nk - 1) - t * BK;  // last visible key, tile-relative
+      finish(slot(t), sc, klim, std::true_type{});
     }
   }
 
