@@ -43,63 +43,10 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQ = 16;  // queries per wave
 
-typedef float f32x4v __attribute__((ext_vector_type(4)));
-
-template <typename T> __device__ __forceinline__ f32x4v mma16(V8<T> a, V8<T> b, f32x4v c);
-template <> __device__ __forceinline__ f32x4v mma16<__bf16>(bf16x8 a, bf16x8 b, f32x4v c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-template <> __device__ __forceinline__ f32x4v mma16<_Float16>(f16x8 a, f16x8 b, f32x4v c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ f32x4v zero4() { return f32x4v{0.f, 0.f, 0.f, 0.f}; }
-
 // The four score tiles of a 32-key tile for one wave (two 16-key C tiles
 // each), transposed (keys x queries): S, ddS (without its scale), dP, dPa.
 struct Scores {
-  f32x4v S[2], ddS[2], dP[2], dPa[2];
-};
-
-// Sum over the four 16-lane groups (lanes holding the same query).
-__device__ __forceinline__ float group4_sum(float x) {
-  x += __shfl_xor(x, 16, 64);
-  return x + __shfl_xor(x, 32, 64);
-}
-
-// Per-lane LDS byte offsets of the 16x16x32 operand fragments read from a
-// swizzled 32 x D tile (2-byte types).
-template <typename T, int D> struct SwzFrags16 {
-  static_assert(sizeof(T) == 2, "2-byte types only");
-  uint32_t row[D / 32];  // score A operand: row l % 16, columns 32 ks + 8 (l / 16) .. +7
-  uint32_t tr[D / 16];   // output A operand of column block db: rows 4 (l / 16) + i / 4
-  __device__ __forceinline__ void init(int lane) {
-    const int n = lane & 15, g = lane >> 4;
-#pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) row[ks] = 2u * (uint32_t)(n * D + 8 * phys_chunk(n, 4 * ks + g));
-    const int r = 4 * g + (n >> 2);
-#pragma unroll
-    for (int db = 0; db < D / 16; ++db) {
-      const int d = 16 * db + 4 * (n & 3);
-      tr[db] = 2u * (uint32_t)(r * D + 8 * phys_chunk(r, d >> 3) + (d & 7));
-    }
-  }
-  // Keys 16 kb + l % 16 of the tile at stage + off, step ks. The swizzle
-  // repeats every 16 rows, so kb is a constant offset.
-  __device__ __forceinline__ V8<T> rowf(uint32_t stage, int off, int kb, int ks) const {
-    const lds_cchar* p = reinterpret_cast<const lds_cchar*>((uintptr_t)(stage + row[ks])) + off + kb * 16 * D * 2;
-    return *reinterpret_cast<const __attribute__((address_space(3))) V8<T>*>(p);
-  }
-  // Column 16 db + l % 16, keys 4 g + {0..3} and 16 + 4 g + {0..3}: within a
-  // 16-lane group, lane i addresses row 4 g + i / 4, columns 16 db + 4 (i % 4)
-  // .. +3, and receives column 16 db + i of the four rows.
-  __device__ __forceinline__ V8<T> trf(uint32_t stage, int off, int db) const {
-    const lds_cchar* a = reinterpret_cast<const lds_cchar*>((uintptr_t)(stage + tr[db])) + off;
-    const i16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a));
-    const i16x4 y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(a + 16 * D * 2));
-    return __builtin_shufflevector(__builtin_bit_cast(V4<T>, x), __builtin_bit_cast(V4<T>, y), 0, 1, 2, 3, 4, 5, 6,
-                                   7);
-  }
+  f32x4 S[2], ddS[2], dP[2], dPa[2];
 };
 
 template <typename T, int D, bool CAUSAL>
@@ -201,7 +148,7 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
   for (int i = 0; i < NST - 1; ++i)
     if (i < nkt) issue(++hi);
 
-  f32x4v acc_a[DB], acc_s[DB], acc_p[DB], acc_o[DB], acc_pv[DB];
+  f32x4 acc_a[DB], acc_s[DB], acc_p[DB], acc_o[DB], acc_pv[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc_a[db] = acc_s[db] = acc_p[db] = acc_o[db] = acc_pv[db] = zero4();
   float dd_acc = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
