@@ -10,11 +10,16 @@
 // With u = dP - D, x = P ddS (ddS including its scale) and
 // X = P (dPa + ddS u):
 //   dQ2 = scale (sum_j P u ddK + sum_j X K - dD sum_j P u K - c sum_j P K),
-//   ddO = sum_j P ddV + sum_j x V - dD sum_j P V,       c = D dD + B,
-// because P (dP2 - B) = X - dD P u - c P and ddP = x - dD P. Every key tile is
-// streamed once; per tile a wave forms the five score products (S, ddS twice,
-// dP, dPa), one exp per pair, and seven output products into five
-// accumulators (dQ2 part, sum P u K, sum P K, ddO part, sum P V).
+//   ddO = sum_j P ddV + sum_j x V - dD O,                c = D dD + B,
+// because P (dP2 - B) = X - dD P u - c P, ddP = x - dD P and sum_j P V = O.
+// The row statistic needs no per-pair work either: expanding B's definition
+// (flash_hog/jax/_pallas_gpu_kernel.py:209-210),
+//   c = D dD + B = sum_j P dPa + sum_j x dP - dD sum_j P dP = <dO, ddO>,
+// since dPa = dO ddV^T and dP = dO V^T. Every key tile is streamed once; per
+// tile a wave forms the five score products (S, ddS twice, dP, dPa), one exp
+// per pair, and six output products into four accumulators (dQ2 part,
+// sum P u K, sum P K, ddO part). The dP accumulator starts at -D, so it ends
+// as u.
 //
 // Sixteen queries per wave. The five accumulators of 32 queries would not fit
 // beside the score tiles in the 256 registers of a wave that shares its SIMD
@@ -148,17 +153,19 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
   for (int i = 0; i < NST - 1; ++i)
     if (i < nkt) issue(++hi);
 
-  f32x4 acc_a[DB], acc_s[DB], acc_p[DB], acc_o[DB], acc_pv[DB];
+  f32x4 acc_a[DB], acc_s[DB], acc_p[DB], acc_o[DB];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) acc_a[db] = acc_s[db] = acc_p[db] = acc_o[db] = acc_pv[db] = zero4();
-  float dd_acc = 0.f, r1 = 0.f, r2 = 0.f, r3 = 0.f;
+  for (int db = 0; db < DB; ++db) acc_a[db] = acc_s[db] = acc_p[db] = acc_o[db] = zero4();
+  float dd_acc = 0.f;
+  const f32x4 init_u = {nD, nD, nD, nD};
 
   // Score tiles of the key tile in slot sa (K at 0, V at kTile, ddK at
-  // 2 kTile, ddV at 3 kTile); kb = 16-key half.
+  // 2 kTile, ddV at 3 kTile); kb = 16-key half. sc.dP ends as u = dP - D.
   auto scores = [&](uint32_t sa, Scores& sc) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      sc.S[kb] = sc.ddS[kb] = sc.dP[kb] = sc.dPa[kb] = zero4();
+      sc.S[kb] = sc.ddS[kb] = sc.dPa[kb] = zero4();
+      sc.dP[kb] = init_u;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const V8<T> kf = fr.rowf(sa, 0, kb, ks);
@@ -183,29 +190,23 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
       float P = exp2_fast(fmaf(sc.S[kb][i], c2, nL2));
       if (MASK && 16 * kb + 4 * g + i > klim) P = 0.f;
       const float x = P * (sc.ddS[kb][i] * scale);  // P ddS
-      const float u = sc.dP[kb][i] + nD;            // dP - D
-      const float pa = P * sc.dPa[kb][i];
+      const float u = sc.dP[kb][i];                 // dP - D
       dd_acc += x;
-      r1 += pa;
-      r2 = fmaf(sc.dP[kb][i], P, r2);
-      r3 = fmaf(sc.dP[kb][i], x, r3);
       vP[e] = P;
       vx[e] = x;
-      vu[e] = P * u;           // P u
-      vX[e] = fmaf(x, u, pa);  // P (dPa + ddS u)
+      vu[e] = P * u;                              // P u
+      vX[e] = fmaf(x, u, P * sc.dPa[kb][i]);      // P (dPa + ddS u)
     }
     const V8<T> oP = cvt8<T>(vP), ox = cvt8<T>(vx), ou = cvt8<T>(vu), oX = cvt8<T>(vX);
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       const V8<T> tK = fr.trf(sa, 0, db);
-      const V8<T> tV = fr.trf(sa, kTile, db);
       acc_a[db] = mma16<T>(fr.trf(sa, 2 * kTile, db), ou, acc_a[db]);
       acc_a[db] = mma16<T>(tK, oX, acc_a[db]);
       acc_s[db] = mma16<T>(tK, ou, acc_s[db]);
       acc_p[db] = mma16<T>(tK, oP, acc_p[db]);
       acc_o[db] = mma16<T>(fr.trf(sa, 3 * kTile, db), oP, acc_o[db]);
-      acc_o[db] = mma16<T>(tV, ox, acc_o[db]);
-      acc_pv[db] = mma16<T>(tV, oP, acc_pv[db]);
+      acc_o[db] = mma16<T>(fr.trf(sa, kTile, db), ox, acc_o[db]);
     }
   };
   auto slot = [&](int kt) { return lds_kv + (uint32_t)((kt % NST) * kStage); };
@@ -269,27 +270,46 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
   }
 
   const float dD = group4_sum(dd_acc);
-  const float Bi = group4_sum(r1) - dD * group4_sum(r2) - Di * dD + group4_sum(r3);
-  const float c = fmaf(Di, dD, Bi);
+  // ddO = acc_o - dD O and c = <dO, ddO>, from this lane's four columns of
+  // each 16-column block (16 db + 4 g + i), summed over the four lane groups.
+  const long roff = qbase + (long)qi * rs;
+  f32x4 y[DB];
+  float cpart = 0.f;
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const int d = 16 * db + 4 * g;
+    V4<T> ov, dov;
+    if (qvalid) {
+      ov = *reinterpret_cast<const V4<T>*>(p.o + roff + d);
+      dov = *reinterpret_cast<const V4<T>*>(p.dout + roff + d);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ov[i] = dov[i] = (T)0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      y[db][i] = acc_o[db][i] - dD * (float)ov[i];
+      cpart = fmaf((float)dov[i], y[db][i], cpart);
+    }
+  }
+  const float c = group4_sum(cpart);
+  const float Bi = c - Di * dD;
   if (qvalid) {
     if (g == 0) {
       p.delta[sbase + qi] = Di;
       p.ddelta[sbase + qi] = dD;
       p.bstat[sbase + qi] = Bi;
     }
-    T* dq2 = p.dq2 + qbase + (long)qi * rs;
-    T* ddo = p.ddo + qbase + (long)qi * rs;
+    T* dq2 = p.dq2 + roff;
+    T* ddo = p.ddo + roff;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       const int d = 16 * db + 4 * g;  // this lane's four output columns
-      f32x4 x, y;
+      f32x4 x;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[i] = scale * (acc_a[db][i] - dD * acc_s[db][i] - c * acc_p[db][i]);
-        y[i] = acc_o[db][i] - dD * acc_pv[db][i];
-      }
+      for (int i = 0; i < 4; ++i) x[i] = scale * (acc_a[db][i] - dD * acc_s[db][i] - c * acc_p[db][i]);
       *reinterpret_cast<V4<T>*>(dq2 + d) = cvt4<T>(x);
-      *reinterpret_cast<V4<T>*>(ddo + d) = cvt4<T>(y);
+      *reinterpret_cast<V4<T>*>(ddo + d) = cvt4<T>(y[db]);
     }
   }
 }
