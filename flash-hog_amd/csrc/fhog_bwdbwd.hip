@@ -57,7 +57,7 @@ template <typename T, int D> struct Occupancy {
 
 // Depth of the LDS ring: tiles stream NST - 1 iterations ahead of their use.
 template <typename T, int D> struct Ring {
-  static constexpr int value = (sizeof(T) == 2 && D == 64) ? 3 : 2;
+  static constexpr int value = (sizeof(T) == 2 && D == 64) ? 4 : 2;
 };
 
 // ----------------------------------------------------------------------------
