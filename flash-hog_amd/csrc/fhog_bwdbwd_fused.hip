@@ -128,7 +128,7 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
   // Wave w streams key-side tensor w (K, V, ddK, ddV) into an NST-stage ring.
   const T* src = (wave == 0 ? p.k : wave == 1 ? p.v : wave == 2 ? p.ddk : p.ddv) + kbase;
   const uint32_t row_bytes = (uint32_t)(rsk * (long)sizeof(T));
-  TileDma<T, D> dma;
+  TileDma<T, D, G::kLoads, kSwzRows> dma;
   dma.init(row_bytes, BK, lane);
   const uint32_t lds_kv = lds_base_u32(s_kv);
   const uint32_t lds_wave = lds_kv + wave * kTile;
@@ -143,7 +143,7 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
     if (nvalid >= BK) {
       dma.issue(dst, gsrc);
     } else {
-      TileDma<T, D> part;
+      TileDma<T, D, G::kLoads, kSwzRows> part;
       part.init(row_bytes, nvalid, lane);
       part.issue(dst, gsrc);
     }

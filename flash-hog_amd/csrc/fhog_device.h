@@ -99,18 +99,18 @@ __device__ __forceinline__ int crow(int r, int g) { return 8 * (r >> 2) + 4 * g 
 //
 // A tile is 32 rows x D columns, stored row-major without padding; each row is
 // split into 16-byte chunks and chunk c of row r is stored at chunk position
-// c ^ swz(r) (within aligned groups of 8 chunks), swz(r) being the bit
-// reversal of (r / 2) mod 8.
-//
-// LDS serves a wave's reads in groups of lanes over 64 four-byte banks
-// (measured on gfx950: 16-byte reads in 16-lane groups, 8-byte transposed
-// reads in 32-lane groups). A 2-byte row of D = 64 is 128 bytes, half the
-// banks, so a row read (16 lanes, 16 consecutive rows, one logical chunk each)
-// is conflict free iff rows of equal parity get distinct keys, which swz gives
-// over any 16 consecutive rows starting at a multiple of 16; the transposed
-// reads (8 rows x 64 bytes per 32 lanes) are conflict free as well. With a key
-// of (r mod 8) rows r and r + 8 collide and the row reads ran at half speed
-// (278 vs 514 bytes per clock per CU).
+// c ^ key(r) (within aligned groups of 8 chunks). Two keys are used, chosen by
+// measurement (a probe timing each read pattern of the kernels alone, 8 waves
+// per CU, ns per wave-wide read per CU; a contiguous 1 KB ds_read_b128 takes
+// 2.17):
+//   kSwzPairs, key = bit reversal of (r / 2) mod 8, for the 32x32x16 operand
+//     reads: row fragments 2.17, transposed fragments 1.36;
+//   kSwzRows, key = r mod 8, for the 16x16x32 operand reads: row fragments
+//     2.07, transposed fragments 1.31.
+// Each key is slow for the other instruction's row reads (3.6-3.7 ns, and the
+// PMC counter SQ_LDS_BANK_CONFLICT reports the extra cycles), so a tile's key
+// follows the instruction that reads it. Both keys repeat every 16 rows, and
+// key(r + 8) = key(r) ^ 1 for kSwzPairs.
 //
 // global_load_lds with 16 bytes per lane writes lane l's data to
 // lds_base + 16 l, so lane l of load t fills chunk position l % CH of row
@@ -119,11 +119,20 @@ __device__ __forceinline__ int crow(int r, int g) { return 8 * (r >> 2) + 4 * g 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) const char lds_cchar;
 
-__device__ __forceinline__ int swz(int r) {
-  const int m = (r >> 1) & 7;
-  return ((m & 1) << 2) | (m & 2) | (m >> 2);
+constexpr int kSwzPairs = 0;
+constexpr int kSwzRows = 1;
+
+template <int SWZ = kSwzPairs> __device__ __forceinline__ int swz(int r) {
+  if constexpr (SWZ == kSwzRows) {
+    return r & 7;
+  } else {
+    const int m = (r >> 1) & 7;
+    return ((m & 1) << 2) | (m & 2) | (m >> 2);
+  }
 }
-__device__ __forceinline__ int phys_chunk(int r, int c) { return (c & ~7) | ((c & 7) ^ swz(r)); }
+template <int SWZ = kSwzPairs> __device__ __forceinline__ int phys_chunk(int r, int c) {
+  return (c & ~7) | ((c & 7) ^ swz<SWZ>(r));
+}
 
 template <typename T, int D> struct SwzTile {
   static constexpr int kRows = 32;
@@ -252,7 +261,7 @@ __device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t
 // only part of a tile). They depend only on the lane, the row stride and the
 // number of valid rows, so a streaming loop computes them once and then only
 // advances the uniform base address per tile.
-template <typename T, int D, int COUNT = SwzTile<T, D>::kLoads> struct TileDma {
+template <typename T, int D, int COUNT = SwzTile<T, D>::kLoads, int SWZ = kSwzPairs> struct TileDma {
   typedef SwzTile<T, D> G;
   static_assert(COUNT >= 1 && COUNT <= G::kLoads, "bad load count");
   uint32_t voff[COUNT];
@@ -267,7 +276,7 @@ template <typename T, int D, int COUNT = SwzTile<T, D>::kLoads> struct TileDma {
     for (int i = 0; i < COUNT; ++i) {
       const int row = (first + i) * G::kRowsPerLoad + lane / G::kChunks;
       const int src_row = min(row, nvalid - 1);
-      voff[i] = (uint32_t)src_row * row_stride_bytes + 16u * (uint32_t)phys_chunk(row, p);
+      voff[i] = (uint32_t)src_row * row_stride_bytes + 16u * (uint32_t)phys_chunk<SWZ>(row, p);
     }
   }
 
@@ -386,12 +395,12 @@ template <typename T, int D> struct SwzFrags16 {
   __device__ __forceinline__ void init(int lane) {
     const int n = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) row[ks] = 2u * (uint32_t)(n * D + 8 * phys_chunk(n, 4 * ks + g));
+    for (int ks = 0; ks < D / 32; ++ks) row[ks] = 2u * (uint32_t)(n * D + 8 * phys_chunk<kSwzRows>(n, 4 * ks + g));
     const int r = 4 * g + (n >> 2);
 #pragma unroll
     for (int db = 0; db < D / 16; ++db) {
       const int d = 16 * db + 4 * (n & 3);
-      tr[db] = 2u * (uint32_t)(r * D + 8 * phys_chunk(r, d >> 3) + (d & 7));
+      tr[db] = 2u * (uint32_t)(r * D + 8 * phys_chunk<kSwzRows>(r, d >> 3) + (d & 7));
     }
   }
   // Keys 16 kb + l % 16 of the tile at stage + off, step ks. The swizzle
