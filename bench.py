@@ -23,6 +23,16 @@ timed steps measure the sustained rate.
 
 Prints one JSON line on stdout; progress goes to stderr.
 
+    python bench.py --configs
+
+times the double backward through the C ABI on each GPU configuration of the
+reference's benchmark set (B4 N2048 H16 D64 bf16 causal; B2 N8192 H16 D128
+bf16 causal; B8 N1000 H12 D64 fp16 non-causal; B1 N32768 H8 D64 bf16 causal)
+and reports per configuration the time, algorithmic TFLOP/s, the two stages'
+times and the peak extra HBM of one call beside the size of one fp32
+N_Q x N_K tensor over all (batch, head) pairs, the least a materialising
+(quadratic) implementation holds. One JSON line per configuration on stdout.
+
     python bench.py --hvp-table {b1,tokens}
 
 times instead the end-to-end causal-attention Hessian-vector product through
@@ -266,6 +276,87 @@ def hvp_table(args):
     return 0
 
 
+CONFIGS = [
+    dict(name="B4 N2048 H16 D64 bf16 causal", batch=4, seq=2048, heads=16, head_dim=64, dtype="bf16", causal=True),
+    dict(name="B2 N8192 H16 D128 bf16 causal", batch=2, seq=8192, heads=16, head_dim=128, dtype="bf16", causal=True),
+    dict(name="B8 N1000 H12 D64 fp16 non-causal", batch=8, seq=1000, heads=12, head_dim=64, dtype="fp16",
+         causal=False, qkv_scale=0.5),
+    dict(name="B1 N32768 H8 D64 bf16 causal", batch=1, seq=32768, heads=8, head_dim=64, dtype="bf16", causal=True),
+]
+
+
+def run_configs(args):
+    """Times the double backward on every GPU configuration (see the module docstring)."""
+    import torch
+
+    from flash_hog import _hip
+
+    dev = torch.device("cuda:0")
+    lib = _hip.lib()
+    dtypes = {"bf16": torch.bfloat16, "fp16": torch.float16}
+    log("| config | ms | alg. TFLOP/s | % bf16 peak | stage 1 ms | stage 2 ms | peak extra HBM | one fp32 N x N tensor |")
+    log("|---|--:|--:|--:|--:|--:|--:|--:|")
+    for c in CONFIGS:
+        B, N, H, D = c["batch"], c["seq"], c["heads"], c["head_dim"]
+        dtype, causal = dtypes[c["dtype"]], c["causal"]
+        scale = 1.0 / math.sqrt(D)
+        x = make_inputs(torch, B, N, H, D, dtype, dev)
+        if c.get("qkv_scale"):
+            for k in ("q", "k", "v"):
+                x[k] = (x[k].float() * c["qkv_scale"]).to(dtype)
+        o, lse = _hip.attention_fwd(x["q"], x["k"], x["v"], causal, scale)
+        outs = [torch.empty_like(x[k]) for k in ("q", "k", "v", "do")]
+        stats = torch.empty((3, B, H, N), device=dev, dtype=torch.float32)
+        stream = torch.cuda.current_stream(dev)
+        s_ptr = stream.cuda_stream
+        common = (x["q"].data_ptr(), x["k"].data_ptr(), x["v"].data_ptr(), o.data_ptr(), x["do"].data_ptr(),
+                  x["ddq"].data_ptr(), x["ddk"].data_ptr(), x["ddv"].data_ptr(), lse.data_ptr(),
+                  *[t.data_ptr() for t in outs], stats[0].data_ptr(), stats[1].data_ptr(), stats[2].data_ptr())
+        dims = (B, N, N, H, H, D, _hip.DTYPE_CODES[dtype], int(causal), scale)
+        step = lambda: _hip.check(lib.fhog_attention_bwdbwd(s_ptr, *common, *dims))
+        stage = lambda k: _hip.check(lib.fhog_attention_bwdbwd_stage(s_ptr, k, *common, *dims))
+        settle(torch, step, args.settle_ms, batch=1)
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        steps = max(3, args.steps // max(1, (N * N * B * H) // (2048 * 2048 * 64)))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+        for e in ev:
+            e[0].record(stream)
+            stage(1)
+            e[1].record(stream)
+            stage(2)
+            e[2].record(stream)
+        torch.cuda.synchronize()
+        s1 = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+        s2 = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+        torch.cuda.reset_peak_memory_stats(dev)
+        base = torch.cuda.memory_allocated(dev)
+        _hip.attention_bwdbwd(x["q"], x["k"], x["v"], o, x["do"], x["ddq"], x["ddk"], x["ddv"], lse, causal, scale)
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated(dev) - base
+        pairs = unmasked_pairs(N, N, causal) * B * H
+        tflops = 24.0 * D * pairs / (ms * 1e-3) / 1e12
+        quad = 4.0 * B * H * N * N
+        row = {"config": c["name"], "ms": round(ms, 4), "alg_tflops": round(tflops, 2),
+               "pct_of_bf16_peak": round(100 * tflops / MI355X_PEAK_BF16_TFLOPS, 2), "stage1_ms": round(s1, 4),
+               "stage2_ms": round(s2, 4), "peak_extra_hbm_bytes": int(peak), "fp32_nxn_bytes": int(quad),
+               "steps": steps}
+        log(f"| {c['name']} | {ms:.3f} | {tflops:.1f} | {100 * tflops / MI355X_PEAK_BF16_TFLOPS:.1f} | {s1:.3f} | "
+            f"{s2:.3f} | {peak / 2**20:.1f} MiB | {quad / 2**30:.1f} GiB |")
+        print(json.dumps(row), flush=True)
+        del x, o, lse, outs, stats
+        torch.cuda.empty_cache()
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description="Flash-HOG double-backward benchmark")
     ap.add_argument("--gpus", type=int, default=1)
@@ -278,6 +369,8 @@ def main(argv=None):
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (PMC byte-counter calibration)")
+    ap.add_argument("--configs", action="store_true",
+                    help="time the double backward on every GPU configuration of the benchmark set instead")
     ap.add_argument("--hvp-table", choices=sorted(HVP_TABLES),
                     help="time the end-to-end HVP on the shapes of one of the reference's HVP tables instead")
     args = ap.parse_args(argv)
@@ -289,6 +382,8 @@ def main(argv=None):
         return 2
     if args.hvp_table:
         return hvp_table(args)
+    if args.configs:
+        return run_configs(args)
 
     import torch
 
