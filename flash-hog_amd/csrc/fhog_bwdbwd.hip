@@ -38,6 +38,9 @@
 // 8 XCDs (each with its own L2); with B H a multiple of 8, XCD x then receives
 // the same eighth of the (batch, head) pairs at every rank, so the blocks that
 // stream one (batch, head) share one L2.
+#include <cmath>
+#include <type_traits>
+
 #include "fhog_device.h"
 #include "fhog_params.h"
 
@@ -331,7 +334,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
 // -(D dD + B)) in LDS. The loop issues no load the compiler tracks, so its
 // only vector-memory waits are the explicit ones.
 // ----------------------------------------------------------------------------
-template <typename T, int D, bool CAUSAL>
+template <typename T, int D, bool CAUSAL, bool PRE>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
 bwdbwd_k_kernel(BwdBwdParams<T> p) {
@@ -396,7 +399,19 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
       }
     }
     const float scale = p.scale;
-    const float c2 = scale * kLog2e;
+    if constexpr (PRE) {
+      // scale is a power of two: K and ddK carry it exactly, so S and ddS come
+      // out of the matrix products already scaled (bit-identical to scaling
+      // them afterwards) and the element-wise step skips one multiply.
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          kf[ks][e] = (T)((float)kf[ks][e] * scale);
+          dkf[ks][e] = (T)((float)dkf[ks][e] * scale);
+        }
+    }
+    const float c2 = PRE ? kLog2e : scale * kLog2e;
 
     SwzFrags<T, D> fr;
     fr.init(lane);
@@ -410,12 +425,18 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
     dma.init(row_bytes, BQ, lane);
     const uint32_t lds_q = lds_base_u32(s_q);
     const uint32_t lds_wave = lds_q + wave * kTile;
+    // Source of the next tile to issue, advanced with the cursor: the next head
+    // of the group is D elements on, the next query tile of the first head
+    // BQ rows on from the first head.
+    const T* gnext = src + (long)qt_begin * BQ * rs;
+    const long row_step = (long)BQ * rs - (long)(grp - 1) * D;
 
     // Wave 3 streams the per-query statistics of each tile with two dword DMAs
     // (lanes 0-31 then 32-63: L and D, then dD and B; rows past nq repeat row
     // nq - 1) into the tile's stage, and once they have landed rewrites them in
     // place as the initial values of the four score accumulators:
-    // -L / scale, -dD / scale, -D, -(D dD + B).
+    // -L / scale, -dD / scale, -D, -(D dD + B) (-L and -dD when K and ddK carry
+    // the scale).
     constexpr int kStatLoads = 2;
     auto issue_stats = [&](int i, GroupCursor c) {
       const int q = min((qt_begin + c.qt) * BQ + n, p.nq - 1);
@@ -429,8 +450,8 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
       if (g == 0) {
         float* st = reinterpret_cast<float*>(s_q + (i % NST) * kStage + 3 * kTile);
         const float L = st[n], Dq = st[BQ + n], dDq = st[2 * BQ + n], Bq = st[3 * BQ + n];
-        st[n] = -L * inv_scale;
-        st[BQ + n] = -dDq * inv_scale;
+        st[n] = PRE ? -L : -L * inv_scale;
+        st[BQ + n] = PRE ? -dDq : -dDq * inv_scale;
         st[2 * BQ + n] = -Dq;
         st[3 * BQ + n] = -fmaf(Dq, dDq, Bq);
       }
@@ -452,23 +473,25 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
         return;
       }
       const int q0t = (qt_begin + c.qt) * BQ;
-      const int nvalid = p.nq - q0t;
       const uint32_t dst = lds_wave + (uint32_t)((i % NST) * kStage);
-      const T* gsrc = src + (long)c.gi * D + (long)q0t * rs;
-      if (nvalid >= BQ) {
-        dma.issue(dst, gsrc);
-      } else {
+      if (q0t + BQ <= p.nq) {
+        dma.issue(dst, gnext);
+      } else {  // the ragged last query tile (offsets made here: registers are scarce)
         TileDma<T, D> part;
-        part.init(row_bytes, nvalid, lane);
-        part.issue(dst, gsrc);
+        part.init(row_bytes, p.nq - q0t, lane);
+        part.issue(dst, gnext);
       }
+    };
+    auto advance = [&](GroupCursor& c) {
+      gnext += c.gi + 1 == grp ? row_step : (long)D;
+      c.next(grp);
     };
     GroupCursor nxt;  // iteration of the next tile to issue
 #pragma unroll
     for (int i = 0; i < NST - 1; ++i)
       if (i < total) {
         issue(i, nxt);
-        nxt.next(grp);
+        advance(nxt);
       }
     if (wave == 3) {
       wait_stats(0);
@@ -481,7 +504,7 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
       __syncthreads();
       if (i + NST - 1 < total) {
         issue(i + NST - 1, nxt);
-        nxt.next(grp);
+        advance(nxt);
       }
       const int q0 = (qt_begin + cur.qt) * BQ;
       const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
@@ -539,7 +562,7 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const int r = 8 * s + e;
-            const float t = ddS[r] * scale;              // ddS - dD
+            const float t = PRE ? ddS[r] : ddS[r] * scale;  // ddS - dD
             const float x = fmaf(dP[r], t, dPa[r]);      // dP2 - B
             vdS[e] = P[r] * dP[r];
             vdS2[e] = P[r] * x;
@@ -603,8 +626,13 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stage
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
-    hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL>), dim3(nkb * p.batch * p.kv_heads), dim3(kThreads), 0,
-                       stream, p);
+    int e2;
+    if (std::is_same_v<T, __bf16> && std::frexp(p.scale, &e2) == 0.5f)  // scale = 2^(e2 - 1)
+      hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, std::is_same_v<T, __bf16>>), dim3(nkb * p.batch * p.kv_heads),
+                         dim3(kThreads), 0, stream, p);
+    else
+      hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, false>), dim3(nkb * p.batch * p.kv_heads), dim3(kThreads), 0,
+                         stream, p);
     return hipGetLastError();
   }
   return hipSuccess;

@@ -35,6 +35,7 @@
 // k' = 8 g + e -> key 4 g + e (e < 4) or 16 + 4 g + e - 4 (e >= 4), and the
 // A operand (the key-side tile, transposed) is read with two
 // ds_read_b64_tr_b16 in the same order.
+#include <cmath>
 #include <type_traits>
 
 #include "fhog_device.h"
@@ -49,12 +50,13 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kQ = 16;  // queries per wave
 
 // The four score tiles of a 32-key tile for one wave (two 16-key C tiles
-// each), transposed (keys x queries): S, ddS (without its scale), dP, dPa.
+// each), transposed (keys x queries): S, ddS (without its scale unless Q and
+// ddQ carry it), dP, dPa.
 struct Scores {
   f32x4 S[2], ddS[2], dP[2], dPa[2];
 };
 
-template <typename T, int D, bool CAUSAL>
+template <typename T, int D, bool CAUSAL, bool PRE>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(2, 2)))
 bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
@@ -107,7 +109,19 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
     }
   }
   const float scale = p.scale;
-  const float c2 = scale * kLog2e;
+  if constexpr (PRE) {
+    // scale is a power of two: Q and ddQ carry it exactly, so S and ddS come
+    // out of the matrix products already scaled (bit-identical to scaling them
+    // afterwards) and the element-wise step skips one multiply.
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        qf[ks][e] = (T)((float)qf[ks][e] * scale);
+        ddqf[ks][e] = (T)((float)ddqf[ks][e] * scale);
+      }
+  }
+  const float c2 = PRE ? kLog2e : scale * kLog2e;
   const float Di = group4_sum(dpart);
   const float nD = -Di;
   const float nL2 = qvalid ? -p.lse[sbase + qi] * kLog2e : 0.f;
@@ -127,6 +141,7 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
 
   // Wave w streams key-side tensor w (K, V, ddK, ddV) into an NST-stage ring.
   const T* src = (wave == 0 ? p.k : wave == 1 ? p.v : wave == 2 ? p.ddk : p.ddv) + kbase;
+  const T* gnext = src;  // source of the next tile to issue (tiles are issued in order)
   const uint32_t row_bytes = (uint32_t)(rsk * (long)sizeof(T));
   TileDma<T, D, G::kLoads, kSwzRows> dma;
   dma.init(row_bytes, BK, lane);
@@ -139,7 +154,8 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
   auto issue = [&](int kt) {
     const int nvalid = p.nk - kt * BK;
     const uint32_t dst = lds_wave + (uint32_t)((kt % NST) * kStage);
-    const T* gsrc = src + (long)kt * BK * rsk;
+    const T* gsrc = gnext;
+    gnext += BK * rsk;
     if (nvalid >= BK) {
       dma.issue(dst, gsrc);
     } else {
@@ -189,7 +205,7 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
       const int kb = e >> 2, i = e & 3;
       float P = exp2_fast(fmaf(sc.S[kb][i], c2, nL2));
       if (MASK && 16 * kb + 4 * g + i > klim) P = 0.f;
-      const float x = P * (sc.ddS[kb][i] * scale);  // P ddS
+      const float x = PRE ? P * sc.ddS[kb][i] : P * (sc.ddS[kb][i] * scale);  // P ddS
       const float u = sc.dP[kb][i];                 // dP - D
       dd_acc += x;
       vP[e] = P;
@@ -319,8 +335,13 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd_stage1_fused(const BwdBwdParams<T>& p, hipStream_t stream) {
   const int nqb = (p.nq + kQ * kWaves - 1) / (kQ * kWaves);
-  hipLaunchKernelGGL((bwdbwd_q_fused_kernel<T, D, CAUSAL>), dim3(nqb * p.batch * p.heads), dim3(kThreads), 0, stream,
-                     p);
+  const dim3 grid(nqb * p.batch * p.heads);
+  int e2;
+  if (std::is_same_v<T, __bf16> && std::frexp(p.scale, &e2) == 0.5f)  // scale = 2^(e2 - 1)
+    hipLaunchKernelGGL((bwdbwd_q_fused_kernel<T, D, CAUSAL, std::is_same_v<T, __bf16>>), grid, dim3(kThreads), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL((bwdbwd_q_fused_kernel<T, D, CAUSAL, false>), grid, dim3(kThreads), 0, stream, p);
   return hipGetLastError();
 }
 
