@@ -337,7 +337,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
 template <typename T, int D, bool CAUSAL, bool PRE>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
-bwdbwd_k_kernel(BwdBwdParams<T> p) {
+bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
@@ -353,263 +353,289 @@ bwdbwd_k_kernel(BwdBwdParams<T> p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, g = lane >> 5;
   const int nbh = p.batch * p.kv_heads;
-  const int kb = blockIdx.x / nbh;  // causal: the longest key columns come first
-  const int bh = blockIdx.x - kb * nbh;
-  const int b = bh / p.kv_heads, hk = bh % p.kv_heads;
-  const int grp = p.heads / p.kv_heads;  // query heads per key/value head
-  const long rs = (long)p.heads * D;      // query-side row stride
-  const long rsk = (long)p.kv_heads * D;  // key-side row stride
-  // query head hk * grp + gi: tensors at qbase + gi * D, statistics at sbase + gi * nq
-  const long qbase = ((long)b * p.nq * p.heads + (long)hk * grp) * D;
-  const long kbase = ((long)b * p.nk * p.kv_heads + hk) * D;
-  const long sbase = ((long)b * p.heads + (long)hk * grp) * p.nq;
-  const int k0 = kb * BKB + wave * 32;
-  const int kj = k0 + n;
-  const bool kvalid = kj < p.nk;
+  const int rank = blockIdx.x / nbh;  // causal: the longest key columns come first
+  const int bh = blockIdx.x - rank * nbh;
+  // With pairs set, workgroup `rank` then also takes the mirror key block
+  // nkb - 1 - rank: causally block r sees the query tiles from r on, so a pair
+  // does about the same work for every r and the grid has no tail of short
+  // blocks.
+  const int nkb = (p.nk + BKB - 1) / BKB;
+  const int nblk = (pairs && nkb - 1 - rank != rank) ? 2 : 1;
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int kb = blk == 0 ? rank : nkb - 1 - rank;
+    if (blk > 0) __syncthreads();  // every wave is done with the previous block's ring
+    const int b = bh / p.kv_heads, hk = bh % p.kv_heads;
+    const int grp = p.heads / p.kv_heads;  // query heads per key/value head
+    const long rs = (long)p.heads * D;      // query-side row stride
+    const long rsk = (long)p.kv_heads * D;  // key-side row stride
+    // query head hk * grp + gi: tensors at qbase + gi * D, statistics at sbase + gi * nq
+    const long qbase = ((long)b * p.nq * p.heads + (long)hk * grp) * D;
+    const long kbase = ((long)b * p.nk * p.kv_heads + hk) * D;
+    const long sbase = ((long)b * p.heads + (long)hk * grp) * p.nq;
+    const int k0 = kb * BKB + wave * 32;
+    const int kj = k0 + n;
+    const bool kvalid = kj < p.nk;
 
-  // Iteration i visits query tile qt_begin + i / grp of query head
-  // hk * grp + i % grp (the group reduction of
-  // flash_hog/jax/_pallas_gpu_kernel.py:333-370, in one ring).
-  const int nqt = (p.nq + BQ - 1) / BQ;
-  const int qt_begin = CAUSAL ? max(0, kb * BKB - p.coff) / BQ : 0;
+    // Iteration i visits query tile qt_begin + i / grp of query head
+    // hk * grp + i % grp (the group reduction of
+    // flash_hog/jax/_pallas_gpu_kernel.py:333-370, in one ring).
+    const int nqt = (p.nq + BQ - 1) / BQ;
+    const int qt_begin = CAUSAL ? max(0, kb * BKB - p.coff) / BQ : 0;
 
-  f32x16 acc_dk2[DT], acc_dv2[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    acc_dk2[dt] = zero16();
-    acc_dv2[dt] = zero16();
-  }
-
-  if (qt_begin < nqt) {
-    // Key-side operands (B of the score products).
-    V8<T> kf[KS], dkf[KS], vf[KS], dvf[KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const long off = kbase + (long)kj * rsk + 16 * ks + 8 * g;
-      if (kvalid) {
-        kf[ks] = *reinterpret_cast<const V8<T>*>(p.k + off);
-        dkf[ks] = *reinterpret_cast<const V8<T>*>(p.ddk + off);
-        vf[ks] = *reinterpret_cast<const V8<T>*>(p.v + off);
-        dvf[ks] = *reinterpret_cast<const V8<T>*>(p.ddv + off);
-      } else {
-        kf[ks] = zero8<T>();
-        dkf[ks] = zero8<T>();
-        vf[ks] = zero8<T>();
-        dvf[ks] = zero8<T>();
-      }
+    f32x16 acc_dk2[DT], acc_dv2[DT];
+  #pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      acc_dk2[dt] = zero16();
+      acc_dv2[dt] = zero16();
     }
-    const float scale = p.scale;
-    if constexpr (PRE) {
-      // scale is a power of two: K and ddK carry it exactly, so S and ddS come
-      // out of the matrix products already scaled (bit-identical to scaling
-      // them afterwards) and the element-wise step skips one multiply.
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          kf[ks][e] = (T)((float)kf[ks][e] * scale);
-          dkf[ks][e] = (T)((float)dkf[ks][e] * scale);
+
+    if (qt_begin < nqt) {
+      // Key-side operands (B of the score products).
+      V8<T> kf[KS], dkf[KS], vf[KS], dvf[KS];
+  #pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const long off = kbase + (long)kj * rsk + 16 * ks + 8 * g;
+        if (kvalid) {
+          kf[ks] = *reinterpret_cast<const V8<T>*>(p.k + off);
+          dkf[ks] = *reinterpret_cast<const V8<T>*>(p.ddk + off);
+          vf[ks] = *reinterpret_cast<const V8<T>*>(p.v + off);
+          dvf[ks] = *reinterpret_cast<const V8<T>*>(p.ddv + off);
+        } else {
+          kf[ks] = zero8<T>();
+          dkf[ks] = zero8<T>();
+          vf[ks] = zero8<T>();
+          dvf[ks] = zero8<T>();
         }
-    }
-    const float c2 = PRE ? kLog2e : scale * kLog2e;
-
-    SwzFrags<T, D> fr;
-    fr.init(lane);
-
-    const int total = (nqt - qt_begin) * grp;
-    // Retire the key-side loads before the ring starts (see bwdbwd_q_kernel).
-    wait_vmem();
-    const T* src = (wave == 0 ? p.q : wave == 1 ? p.dout : p.ddq) + qbase;
-    const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
-    TileDma<T, D> dma;
-    dma.init(row_bytes, BQ, lane);
-    const uint32_t lds_q = lds_base_u32(s_q);
-    const uint32_t lds_wave = lds_q + wave * kTile;
-    // Source of the next tile to issue, advanced with the cursor: the next head
-    // of the group is D elements on, the next query tile of the first head
-    // BQ rows on from the first head.
-    const T* gnext = src + (long)qt_begin * BQ * rs;
-    const long row_step = (long)BQ * rs - (long)(grp - 1) * D;
-
-    // Wave 3 streams the per-query statistics of each tile with two dword DMAs
-    // (lanes 0-31 then 32-63: L and D, then dD and B; rows past nq repeat row
-    // nq - 1) into the tile's stage, and once they have landed rewrites them in
-    // place as the initial values of the four score accumulators:
-    // -L / scale, -dD / scale, -D, -(D dD + B) (-L and -dD when K and ddK carry
-    // the scale).
-    constexpr int kStatLoads = 2;
-    auto issue_stats = [&](int i, GroupCursor c) {
-      const int q = min((qt_begin + c.qt) * BQ + n, p.nq - 1);
-      const long sb = sbase + (long)c.gi * p.nq;
-      const uint32_t dst = lds_base_u32(s_q) + (uint32_t)((i % NST) * kStage + 3 * kTile);
-      dma4((g ? p.delta : p.lse) + sb + q, dst);
-      dma4((g ? p.bstat : p.ddelta) + sb + q, dst + 256);
-    };
-    const float inv_scale = 1.0f / scale;
-    auto finish_stats = [&](int i) {
-      if (g == 0) {
-        float* st = reinterpret_cast<float*>(s_q + (i % NST) * kStage + 3 * kTile);
-        const float L = st[n], Dq = st[BQ + n], dDq = st[2 * BQ + n], Bq = st[3 * BQ + n];
-        st[n] = PRE ? -L : -L * inv_scale;
-        st[BQ + n] = PRE ? -dDq : -dDq * inv_scale;
-        st[2 * BQ + n] = -Dq;
-        st[3 * BQ + n] = -fmaf(Dq, dDq, Bq);
       }
-    };
-    // Waits (wave 3) until the statistics of tile i have landed: the DMAs of
-    // later tiles, at most NST - 2 of them, may still be in flight.
-    auto wait_stats = [&](int i) {
-      if constexpr (NST >= 3) {
-        if (i + NST - 2 < total) {
-          wait_vmem_le<(NST - 2) * kStatLoads>();
+      const float scale = p.scale;
+      if constexpr (PRE) {
+        // scale is a power of two: K and ddK carry it exactly, so S and ddS come
+        // out of the matrix products already scaled (bit-identical to scaling
+        // them afterwards) and the element-wise step skips one multiply.
+  #pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            kf[ks][e] = (T)((float)kf[ks][e] * scale);
+            dkf[ks][e] = (T)((float)dkf[ks][e] * scale);
+          }
+      }
+      const float c2 = PRE ? kLog2e : scale * kLog2e;
+
+      SwzFrags<T, D> fr;
+      fr.init(lane);
+
+      const int total = (nqt - qt_begin) * grp;
+      // Retire the key-side loads before the ring starts (see bwdbwd_q_kernel).
+      wait_vmem();
+      const T* src = (wave == 0 ? p.q : wave == 1 ? p.dout : p.ddq) + qbase;
+      const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
+      TileDma<T, D> dma;
+      dma.init(row_bytes, BQ, lane);
+      const uint32_t lds_q = lds_base_u32(s_q);
+      const uint32_t lds_wave = lds_q + wave * kTile;
+      // Source of the next tile to issue, advanced with the cursor: the next head
+      // of the group is D elements on, the next query tile of the first head
+      // BQ rows on from the first head.
+      const T* gnext = src + (long)qt_begin * BQ * rs;
+      const long row_step = (long)BQ * rs - (long)(grp - 1) * D;
+
+      // Wave 3 streams the per-query statistics of each tile with two dword DMAs
+      // (lanes 0-31 then 32-63: L and D, then dD and B; rows past nq repeat row
+      // nq - 1) into the tile's stage, and once they have landed rewrites them in
+      // place as the initial values of the four score accumulators:
+      // -L / scale, -dD / scale, -D, -(D dD + B) (-L and -dD when K and ddK carry
+      // the scale).
+      constexpr int kStatLoads = 4;  // two per lane half
+      auto issue_stats = [&](int i, GroupCursor c) {
+        // uniform row base plus a per-lane offset; each lane half loads its own tensor
+        const uint32_t off = 4u * (uint32_t)min((qt_begin + c.qt) * BQ + n, p.nq - 1);
+        const long sb = sbase + (long)c.gi * p.nq;
+        const uint32_t dst = lds_base_u32(s_q) + (uint32_t)((i % NST) * kStage + 3 * kTile);
+        if (g == 0) {
+          dma4s(p.lse + sb, off, dst);
+          dma4s(p.ddelta + sb, off, dst + 256);
+        } else {
+          dma4s(p.delta + sb, off, dst);
+          dma4s(p.bstat + sb, off, dst + 256);
+        }
+      };
+      const float inv_scale = 1.0f / scale;
+      auto finish_stats = [&](int i) {
+        if (g == 0) {
+          float* st = reinterpret_cast<float*>(s_q + (i % NST) * kStage + 3 * kTile);
+          const float L = st[n], Dq = st[BQ + n], dDq = st[2 * BQ + n], Bq = st[3 * BQ + n];
+          st[n] = PRE ? -L : -L * inv_scale;
+          st[BQ + n] = PRE ? -dDq : -dDq * inv_scale;
+          st[2 * BQ + n] = -Dq;
+          st[3 * BQ + n] = -fmaf(Dq, dDq, Bq);
+        }
+      };
+      // Waits (wave 3) until the statistics of tile i have landed: the DMAs of
+      // later tiles, at most NST - 2 of them, may still be in flight.
+      auto wait_stats = [&](int i) {
+        if constexpr (NST >= 3) {
+          if (i + NST - 2 < total) {
+            wait_vmem_le<(NST - 2) * kStatLoads>();
+            return;
+          }
+        }
+        wait_vmem_le<0>();
+      };
+      auto issue = [&](int i, GroupCursor c) {
+        if (wave == 3) {
+          issue_stats(i, c);
           return;
         }
-      }
-      wait_vmem_le<0>();
-    };
-    auto issue = [&](int i, GroupCursor c) {
+        const int q0t = (qt_begin + c.qt) * BQ;
+        const uint32_t dst = lds_wave + (uint32_t)((i % NST) * kStage);
+        if (q0t + BQ <= p.nq) {
+          dma.issue(dst, gnext);
+        } else {  // the ragged last query tile (offsets made here: registers are scarce)
+          TileDma<T, D> part;
+          part.init(row_bytes, p.nq - q0t, lane);
+          part.issue(dst, gnext);
+        }
+      };
+      auto advance = [&](GroupCursor& c) {
+        gnext += c.gi + 1 == grp ? row_step : (long)D;
+        c.next(grp);
+      };
+      GroupCursor nxt;  // iteration of the next tile to issue
+  #pragma unroll
+      for (int i = 0; i < NST - 1; ++i)
+        if (i < total) {
+          issue(i, nxt);
+          advance(nxt);
+        }
       if (wave == 3) {
-        issue_stats(i, c);
-        return;
+        wait_stats(0);
+        finish_stats(0);
       }
-      const int q0t = (qt_begin + c.qt) * BQ;
-      const uint32_t dst = lds_wave + (uint32_t)((i % NST) * kStage);
-      if (q0t + BQ <= p.nq) {
-        dma.issue(dst, gnext);
-      } else {  // the ragged last query tile (offsets made here: registers are scarce)
-        TileDma<T, D> part;
-        part.init(row_bytes, p.nq - q0t, lane);
-        part.issue(dst, gnext);
+
+      GroupCursor cur;  // iteration i
+      for (int i = 0; i < total; ++i, cur.next(grp)) {
+        if (wave < 3) wait_tile<NST, G::kLoads>(i, total);
+        __syncthreads();
+        if (i + NST - 1 < total) {
+          issue(i + NST - 1, nxt);
+          advance(nxt);
+        }
+        const int q0 = (qt_begin + cur.qt) * BQ;
+        const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
+        if (active) {
+          const char* st = s_q + (i % NST) * kStage;
+          const uint32_t sa = lds_q + (uint32_t)((i % NST) * kStage);  // tiles: Q, dO, ddQ
+          const float* sc = reinterpret_cast<const float*>(st + 3 * kTile);
+          // The accumulators start at the per-query constants (register r holds
+          // query 8 (r / 4) + 4 g + r % 4 of the tile), so they end as
+          //   S' = S_raw - L / scale, ddS' = ddS_raw - dD / scale,
+          //   u = dP - D, dPa' = dPa - (D dD + B).
+          f32x16 S, ddS, dP, dPa;
+  #pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            const int m0 = 8 * a + 4 * g;
+            const f32x4 c0 = *reinterpret_cast<const f32x4*>(sc + m0);
+            const f32x4 c1 = *reinterpret_cast<const f32x4*>(sc + BQ + m0);
+            const f32x4 c2v = *reinterpret_cast<const f32x4*>(sc + 2 * BQ + m0);
+            const f32x4 c3 = *reinterpret_cast<const f32x4*>(sc + 3 * BQ + m0);
+  #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              S[4 * a + j] = c0[j];
+              ddS[4 * a + j] = c1[j];
+              dP[4 * a + j] = c2v[j];
+              dPa[4 * a + j] = c3[j];
+            }
+          }
+  #pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            const V8<T> qa = fr.rowf(sa, 0, ks);
+            const V8<T> dqa = fr.rowf(sa, 2 * kTile, ks);
+            const V8<T> doa = fr.rowf(sa, kTile, ks);
+            S = mma<T>(qa, kf[ks], S);
+            ddS = mma<T>(dqa, kf[ks], ddS);
+            ddS = mma<T>(qa, dkf[ks], ddS);
+            dP = mma<T>(doa, vf[ks], dP);
+            dPa = mma<T>(doa, dvf[ks], dPa);
+          }
+          f32x16 P;
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) P[r] = exp2_fast(S[r] * c2);
+          const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31 - p.coff);
+          if (need_mask) {
+            // visible iff query >= key - coff (causal) and query < nq
+            const int qlo = (CAUSAL ? kj - p.coff : 0) - q0, qhi = p.nq - q0;
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int m = crow(r, g);
+              if (m < qlo || m >= qhi) P[r] = 0.f;
+            }
+          }
+  #pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            f32x8 vdS, vdS2, vddP;
+  #pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int r = 8 * s + e;
+              const float t = PRE ? ddS[r] : ddS[r] * scale;  // ddS - dD
+              const float x = fmaf(dP[r], t, dPa[r]);      // dP2 - B
+              vdS[e] = P[r] * dP[r];
+              vdS2[e] = P[r] * x;
+              vddP[e] = P[r] * t;
+            }
+            const V8<T> oS = cvt8<T>(vdS);
+            const V8<T> oS2 = cvt8<T>(vdS2);
+            const V8<T> odP = cvt8<T>(vddP);
+  #pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+              acc_dk2[dt] = mma<T>(fr.trf(sa, 2 * kTile, dt, s), oS, acc_dk2[dt]);
+              acc_dk2[dt] = mma<T>(fr.trf(sa, 0, dt, s), oS2, acc_dk2[dt]);
+              acc_dv2[dt] = mma<T>(fr.trf(sa, kTile, dt, s), odP, acc_dv2[dt]);
+            }
+          }
+        }
+        // Tile i + 1's statistics are read after the next barrier.
+        if (wave == 3 && i + 1 < total) {
+          wait_stats(i + 1);
+          finish_stats(i + 1);
+        }
       }
-    };
-    auto advance = [&](GroupCursor& c) {
-      gnext += c.gi + 1 == grp ? row_step : (long)D;
-      c.next(grp);
-    };
-    GroupCursor nxt;  // iteration of the next tile to issue
-#pragma unroll
-    for (int i = 0; i < NST - 1; ++i)
-      if (i < total) {
-        issue(i, nxt);
-        advance(nxt);
-      }
-    if (wave == 3) {
-      wait_stats(0);
-      finish_stats(0);
     }
 
-    GroupCursor cur;  // iteration i
-    for (int i = 0; i < total; ++i, cur.next(grp)) {
-      if (wave < 3) wait_tile<NST, G::kLoads>(i, total);
-      __syncthreads();
-      if (i + NST - 1 < total) {
-        issue(i + NST - 1, nxt);
-        advance(nxt);
-      }
-      const int q0 = (qt_begin + cur.qt) * BQ;
-      const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
-      if (active) {
-        const char* st = s_q + (i % NST) * kStage;
-        const uint32_t sa = lds_q + (uint32_t)((i % NST) * kStage);  // tiles: Q, dO, ddQ
-        const float* sc = reinterpret_cast<const float*>(st + 3 * kTile);
-        // The accumulators start at the per-query constants (register r holds
-        // query 8 (r / 4) + 4 g + r % 4 of the tile), so they end as
-        //   S' = S_raw - L / scale, ddS' = ddS_raw - dD / scale,
-        //   u = dP - D, dPa' = dPa - (D dD + B).
-        f32x16 S, ddS, dP, dPa;
-#pragma unroll
+    if (kvalid) {
+      const float scale = p.scale;
+      T* dk2 = p.dk2 + kbase + (long)kj * rsk;
+      T* dv2 = p.dv2 + kbase + (long)kj * rsk;
+  #pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+  #pragma unroll
         for (int a = 0; a < 4; ++a) {
-          const int m0 = 8 * a + 4 * g;
-          const f32x4 c0 = *reinterpret_cast<const f32x4*>(sc + m0);
-          const f32x4 c1 = *reinterpret_cast<const f32x4*>(sc + BQ + m0);
-          const f32x4 c2v = *reinterpret_cast<const f32x4*>(sc + 2 * BQ + m0);
-          const f32x4 c3 = *reinterpret_cast<const f32x4*>(sc + 3 * BQ + m0);
-#pragma unroll
+          const int d = 32 * dt + 8 * a + 4 * g;
+          f32x4 x, y;
+  #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            S[4 * a + j] = c0[j];
-            ddS[4 * a + j] = c1[j];
-            dP[4 * a + j] = c2v[j];
-            dPa[4 * a + j] = c3[j];
+            x[j] = acc_dk2[dt][4 * a + j] * scale;
+            y[j] = acc_dv2[dt][4 * a + j];
           }
+          *reinterpret_cast<V4<T>*>(dk2 + d) = cvt4<T>(x);
+          *reinterpret_cast<V4<T>*>(dv2 + d) = cvt4<T>(y);
         }
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const V8<T> qa = fr.rowf(sa, 0, ks);
-          const V8<T> dqa = fr.rowf(sa, 2 * kTile, ks);
-          const V8<T> doa = fr.rowf(sa, kTile, ks);
-          S = mma<T>(qa, kf[ks], S);
-          ddS = mma<T>(dqa, kf[ks], ddS);
-          ddS = mma<T>(qa, dkf[ks], ddS);
-          dP = mma<T>(doa, vf[ks], dP);
-          dPa = mma<T>(doa, dvf[ks], dPa);
-        }
-        f32x16 P;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) P[r] = exp2_fast(S[r] * c2);
-        const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31 - p.coff);
-        if (need_mask) {
-          // visible iff query >= key - coff (causal) and query < nq
-          const int qlo = (CAUSAL ? kj - p.coff : 0) - q0, qhi = p.nq - q0;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int m = crow(r, g);
-            if (m < qlo || m >= qhi) P[r] = 0.f;
-          }
-        }
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          f32x8 vdS, vdS2, vddP;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int r = 8 * s + e;
-            const float t = PRE ? ddS[r] : ddS[r] * scale;  // ddS - dD
-            const float x = fmaf(dP[r], t, dPa[r]);      // dP2 - B
-            vdS[e] = P[r] * dP[r];
-            vdS2[e] = P[r] * x;
-            vddP[e] = P[r] * t;
-          }
-          const V8<T> oS = cvt8<T>(vdS);
-          const V8<T> oS2 = cvt8<T>(vdS2);
-          const V8<T> odP = cvt8<T>(vddP);
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            acc_dk2[dt] = mma<T>(fr.trf(sa, 2 * kTile, dt, s), oS, acc_dk2[dt]);
-            acc_dk2[dt] = mma<T>(fr.trf(sa, 0, dt, s), oS2, acc_dk2[dt]);
-            acc_dv2[dt] = mma<T>(fr.trf(sa, kTile, dt, s), odP, acc_dv2[dt]);
-          }
-        }
-      }
-      // Tile i + 1's statistics are read after the next barrier.
-      if (wave == 3 && i + 1 < total) {
-        wait_stats(i + 1);
-        finish_stats(i + 1);
-      }
-    }
-  }
-
-  if (kvalid) {
-    const float scale = p.scale;
-    T* dk2 = p.dk2 + kbase + (long)kj * rsk;
-    T* dv2 = p.dv2 + kbase + (long)kj * rsk;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const int d = 32 * dt + 8 * a + 4 * g;
-        f32x4 x, y;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          x[j] = acc_dk2[dt][4 * a + j] * scale;
-          y[j] = acc_dv2[dt][4 * a + j];
-        }
-        *reinterpret_cast<V4<T>*>(dk2 + d) = cvt4<T>(x);
-        *reinterpret_cast<V4<T>*>(dv2 + d) = cvt4<T>(y);
       }
     }
   }
 }
 
 }  // namespace
+
+// Workgroups of 4 waves resident on the current device at once, at `waves`
+// waves per SIMD (0 if the device cannot be queried).
+static int resident_workgroups(int waves) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  return cus * waves;
+}
 
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stages) {
@@ -626,13 +652,15 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stage
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
+    // Pair causal key blocks when the grid outnumbers the resident workgroups.
+    const int pairs = CAUSAL && nkb * p.batch * p.kv_heads > resident_workgroups(Occupancy<T, D>::value);
+    const dim3 grid((pairs ? (nkb + 1) / 2 : nkb) * p.batch * p.kv_heads);
     int e2;
     if (std::is_same_v<T, __bf16> && std::frexp(p.scale, &e2) == 0.5f)  // scale = 2^(e2 - 1)
-      hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, std::is_same_v<T, __bf16>>), dim3(nkb * p.batch * p.kv_heads),
-                         dim3(kThreads), 0, stream, p);
+      hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, std::is_same_v<T, __bf16>>), grid, dim3(kThreads), 0, stream, p,
+                         pairs);
     else
-      hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, false>), dim3(nkb * p.batch * p.kv_heads), dim3(kThreads), 0,
-                         stream, p);
+      hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, false>), grid, dim3(kThreads), 0, stream, p, pairs);
     return hipGetLastError();
   }
   return hipSuccess;
