@@ -7,7 +7,7 @@ import math
 import numpy as np
 import torch
 
-# Per-output tolerance on max|a - r| / max|r| (the north-star parity bar):
+# Per-output tolerance on max|a - r| / max|r| (the parity bar of this path):
 # fp32 runs below 1e-3; bf16/fp16 runs below 2e-2 against an fp32-or-better reference.
 TOL = {torch.float32: 1e-3, torch.float16: 2e-2, torch.bfloat16: 2e-2}
 

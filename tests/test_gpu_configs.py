@@ -16,8 +16,8 @@ fixed subset of heads otherwise, and through properties that hold at any size:
 - the extra device memory of a call (outputs plus three fp32 row vectors) grows
   linearly in N; no (N, N) buffer is allocated.
 
-Tolerance: max|a - r| / max|r| < 2e-2 for bf16 and fp16 inputs (the north-star
-bar for 2-byte runs against an fp32 reference).
+Tolerance: max|a - r| / max|r| < 2e-2 for bf16 and fp16 inputs (the parity bar
+for 2-byte runs against an fp32 reference).
 """
 
 from __future__ import annotations
