@@ -36,7 +36,7 @@ template <typename T, int D> struct Occupancy {
 template <typename T, int D, bool CAUSAL>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
-bwd_q_kernel(BwdParams<T> p) {
+bwd_q_kernel(BwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
@@ -53,9 +53,9 @@ bwd_q_kernel(BwdParams<T> p) {
   const int n = lane & 31, g = lane >> 5;
   const int nqb = (p.nq + BQ - 1) / BQ;
   const int nbh = p.batch * p.heads;
-  const int rank = blockIdx.x / nbh;
-  const int bh = blockIdx.x - rank * nbh;
-  const int qb = CAUSAL ? nqb - 1 - rank : rank;
+  const GridSlot gs = grid_slot(blockIdx.x, nbh, nqb, chunk);
+  const int bh = gs.pair;
+  const int qb = CAUSAL ? nqb - 1 - gs.rank : gs.rank;  // causal: the longest query rows first
   const int b = bh / p.heads, h = bh % p.heads;
   const int hk = h / (p.heads / p.kv_heads);
   const long rs = (long)p.heads * D;      // query-side row stride
@@ -185,7 +185,7 @@ bwd_q_kernel(BwdParams<T> p) {
 template <typename T, int D, bool CAUSAL>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
-bwd_k_kernel(BwdParams<T> p) {
+bwd_k_kernel(BwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
@@ -206,8 +206,10 @@ bwd_k_kernel(BwdParams<T> p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, g = lane >> 5;
   const int nbh = p.batch * p.kv_heads;
-  const int kb = blockIdx.x / nbh;  // causal: the longest key columns come first
-  const int bh = blockIdx.x - kb * nbh;
+  const int nkb = (p.nk + 32 * kWaves - 1) / (32 * kWaves);
+  const GridSlot gs = grid_slot(blockIdx.x, nbh, nkb, chunk);
+  const int kb = gs.rank;  // causal: the longest key columns come first
+  const int bh = gs.pair;
   const int b = bh / p.kv_heads, hk = bh % p.kv_heads;
   const int grp = p.heads / p.kv_heads;  // query heads per key/value head
   const long rs = (long)p.heads * D;      // query-side row stride
@@ -385,10 +387,14 @@ template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t stream) {
   const int nqb = (p.nq + 32 * kWaves - 1) / (32 * kWaves);
   const int nkb = (p.nk + 32 * kWaves - 1) / (32 * kWaves);
-  hipLaunchKernelGGL((bwd_q_kernel<T, D, CAUSAL>), dim3(nqb * p.batch * p.heads), dim3(kThreads), 0, stream, p);
+  const int resident = resident_workgroups(Occupancy<T, D>::value);
+  const int nq_pairs = p.batch * p.heads, nk_pairs = p.batch * p.kv_heads;
+  hipLaunchKernelGGL((bwd_q_kernel<T, D, CAUSAL>), dim3(nqb * nq_pairs), dim3(kThreads), 0, stream, p,
+                     grid_chunk(nq_pairs, nqb, resident));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL>), dim3(nkb * p.batch * p.kv_heads), dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL>), dim3(nkb * nk_pairs), dim3(kThreads), 0, stream, p,
+                     grid_chunk(nk_pairs, nkb, resident));
   return hipGetLastError();
 }
 

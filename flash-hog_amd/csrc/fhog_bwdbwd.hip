@@ -77,7 +77,7 @@ template <typename T, int D> struct Ring {
 template <typename T, int D, bool CAUSAL>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
-bwdbwd_q_kernel(BwdBwdParams<T> p) {
+bwdbwd_q_kernel(BwdBwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;       // 16-deep steps over the head dim
   constexpr int DT = D / 32;       // 32-wide output column blocks
@@ -93,9 +93,9 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
   const int n = lane & 31, g = lane >> 5;
   const int nqb = (p.nq + BQ - 1) / BQ;
   const int nbh = p.batch * p.heads;
-  const int rank = blockIdx.x / nbh;
-  const int bh = blockIdx.x - rank * nbh;
-  const int qb = CAUSAL ? nqb - 1 - rank : rank;
+  const GridSlot gs = grid_slot(blockIdx.x, nbh, nqb, chunk);
+  const int bh = gs.pair;
+  const int qb = CAUSAL ? nqb - 1 - gs.rank : gs.rank;  // causal: the longest query rows first
   const int b = bh / p.heads, h = bh % p.heads;
   const int hk = h / (p.heads / p.kv_heads);
   const long rs = (long)p.heads * D;      // query-side row stride
@@ -337,7 +337,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p) {
 template <typename T, int D, bool CAUSAL, bool PRE>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
-bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs) {
+bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
@@ -353,13 +353,14 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 31, g = lane >> 5;
   const int nbh = p.batch * p.kv_heads;
-  const int rank = blockIdx.x / nbh;  // causal: the longest key columns come first
-  const int bh = blockIdx.x - rank * nbh;
-  // With pairs set, workgroup `rank` then also takes the mirror key block
+  const int nkb = (p.nk + BKB - 1) / BKB;
+  // Key block `rank` of pair bh (causal: the longest key columns come first).
+  // With pairs set, the workgroup then also takes the mirror key block
   // nkb - 1 - rank: causally block r sees the query tiles from r on, so a pair
   // does about the same work for every r and the grid has no tail of short
   // blocks.
-  const int nkb = (p.nk + BKB - 1) / BKB;
+  const GridSlot slot = grid_slot(blockIdx.x, nbh, pairs ? (nkb + 1) / 2 : nkb, chunk);
+  const int rank = slot.rank, bh = slot.pair;
   const int nblk = (pairs && nkb - 1 - rank != rank) ? 2 : 1;
   for (int blk = 0; blk < nblk; ++blk) {
     const int kb = blk == 0 ? rank : nkb - 1 - rank;
@@ -627,16 +628,6 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs) {
 
 }  // namespace
 
-// Workgroups of 4 waves resident on the current device at once, at `waves`
-// waves per SIMD (0 if the device cannot be queried).
-static int resident_workgroups(int waves) {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 0;
-  return cus * waves;
-}
-
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stages) {
   const int nqb = (p.nq + 32 * kWaves - 1) / (32 * kWaves);
@@ -646,21 +637,27 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stage
     if constexpr (sizeof(T) == 2 && D == 64) {
       e = launch_bwdbwd_stage1_fused<T, D, CAUSAL>(p, stream);
     } else {
-      hipLaunchKernelGGL((bwdbwd_q_kernel<T, D, CAUSAL>), dim3(nqb * p.batch * p.heads), dim3(kThreads), 0, stream, p);
+      const int npairs = p.batch * p.heads;
+      hipLaunchKernelGGL((bwdbwd_q_kernel<T, D, CAUSAL>), dim3(nqb * npairs), dim3(kThreads), 0, stream, p,
+                         grid_chunk(npairs, nqb, resident_workgroups(Occupancy<T, D>::value)));
       e = hipGetLastError();
     }
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
     // Pair causal key blocks when the grid outnumbers the resident workgroups.
-    const int pairs = CAUSAL && nkb * p.batch * p.kv_heads > resident_workgroups(Occupancy<T, D>::value);
-    const dim3 grid((pairs ? (nkb + 1) / 2 : nkb) * p.batch * p.kv_heads);
+    const int npairs = p.batch * p.kv_heads;
+    const int resident = resident_workgroups(Occupancy<T, D>::value);
+    const int pairs = CAUSAL && nkb * npairs > resident;
+    const int nranks = pairs ? (nkb + 1) / 2 : nkb;
+    const int chunk = grid_chunk(npairs, nranks, resident);
+    const dim3 grid(nranks * npairs);
     int e2;
     if (std::is_same_v<T, __bf16> && std::frexp(p.scale, &e2) == 0.5f)  // scale = 2^(e2 - 1)
       hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, std::is_same_v<T, __bf16>>), grid, dim3(kThreads), 0, stream, p,
-                         pairs);
+                         pairs, chunk);
     else
-      hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, false>), grid, dim3(kThreads), 0, stream, p, pairs);
+      hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, false>), grid, dim3(kThreads), 0, stream, p, pairs, chunk);
     return hipGetLastError();
   }
   return hipSuccess;

@@ -59,7 +59,7 @@ struct Scores {
 template <typename T, int D, bool CAUSAL, bool PRE>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(2, 2)))
-bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
+bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 32;       // 32-deep steps over the head dim (score products)
   constexpr int DB = D / 16;       // 16-wide output column blocks
@@ -75,9 +75,9 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
   const int n = lane & 15, g = lane >> 4;
   const int nqb = (p.nq + BQ - 1) / BQ;
   const int nbh = p.batch * p.heads;
-  const int rank = blockIdx.x / nbh;
-  const int bh = blockIdx.x - rank * nbh;
-  const int qb = CAUSAL ? nqb - 1 - rank : rank;
+  const GridSlot gs = grid_slot(blockIdx.x, nbh, nqb, chunk);
+  const int bh = gs.pair;
+  const int qb = CAUSAL ? nqb - 1 - gs.rank : gs.rank;  // causal: the longest query rows first
   const int b = bh / p.heads, h = bh % p.heads;
   const int hk = h / (p.heads / p.kv_heads);
   const long rs = (long)p.heads * D;      // query-side row stride
@@ -335,13 +335,15 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p) {
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd_stage1_fused(const BwdBwdParams<T>& p, hipStream_t stream) {
   const int nqb = (p.nq + kQ * kWaves - 1) / (kQ * kWaves);
-  const dim3 grid(nqb * p.batch * p.heads);
+  const int npairs = p.batch * p.heads;
+  const int chunk = grid_chunk(npairs, nqb, resident_workgroups(2));
+  const dim3 grid(nqb * npairs);
   int e2;
   if (std::is_same_v<T, __bf16> && std::frexp(p.scale, &e2) == 0.5f)  // scale = 2^(e2 - 1)
     hipLaunchKernelGGL((bwdbwd_q_fused_kernel<T, D, CAUSAL, std::is_same_v<T, __bf16>>), grid, dim3(kThreads), 0,
-                       stream, p);
+                       stream, p, chunk);
   else
-    hipLaunchKernelGGL((bwdbwd_q_fused_kernel<T, D, CAUSAL, false>), grid, dim3(kThreads), 0, stream, p);
+    hipLaunchKernelGGL((bwdbwd_q_fused_kernel<T, D, CAUSAL, false>), grid, dim3(kThreads), 0, stream, p, chunk);
   return hipGetLastError();
 }
 

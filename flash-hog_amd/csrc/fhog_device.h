@@ -421,4 +421,46 @@ template <typename T, int D> struct SwzFrags16 {
   }
 };
 
+
+// Grid order of the sequence-tiled kernels. A workgroup takes one (batch,
+// head) pair and one block along the sequence, its `rank` (for causal grids
+// rank 0 is the block with the most unmasked tiles). Pairs are taken in
+// chunks of `chunk`: all ranks of one chunk precede the next chunk, so the
+// blocks of one pair run close together in time and share the pair's streamed
+// tiles in L2; with `chunk` a multiple of 8 they also run on one XCD, since
+// workgroup i goes to XCD i mod 8. chunk = npairs is the plain rank-major
+// order over all pairs.
+struct GridSlot {
+  int rank, pair;
+};
+__device__ __forceinline__ GridSlot grid_slot(int wg, int npairs, int nranks, int chunk) {
+  const int per = chunk * nranks;
+  const int c = wg / per;
+  const int rem = wg - c * per;
+  const int n = min(chunk, npairs - c * chunk);  // pairs in this chunk (the last may be short)
+  const int rank = rem / n;
+  return GridSlot{rank, c * chunk + rem - rank * n};
+}
+
+// Workgroups of 4 waves resident on the current device at once, at `waves`
+// waves per SIMD (0 if the device cannot be queried).
+inline int resident_workgroups(int waves) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  return cus * waves;
+}
+
+// The chunk for grid_slot. A grid of at most 8 rounds of resident
+// workgroups keeps the rank-major order, whose last round holds the blocks
+// with the least work; a longer grid takes about one round per chunk (at
+// least 8 pairs, a multiple of 8), so that the streamed tiles of the pairs
+// in flight stay in L2 instead of being fetched again by every block.
+inline int grid_chunk(int npairs, int nranks, int resident) {
+  if (resident <= 0 || (long)npairs * nranks <= 8L * resident) return npairs;
+  const int c = resident / nranks / 8 * 8;
+  return c < 8 ? 8 : (c < npairs ? c : npairs);
+}
+
 }  // namespace fhog

@@ -32,7 +32,7 @@ template <typename T, int D> struct Occupancy {
 template <typename T, int D, bool CAUSAL>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
-fwd_kernel(FwdParams<T> p) {
+fwd_kernel(FwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
@@ -49,9 +49,9 @@ fwd_kernel(FwdParams<T> p) {
   const int n = lane & 31, g = lane >> 5;
   const int nqb = (p.nq + BQ - 1) / BQ;
   const int nbh = p.batch * p.heads;
-  const int rank = blockIdx.x / nbh;
-  const int bh = blockIdx.x - rank * nbh;
-  const int qb = CAUSAL ? nqb - 1 - rank : rank;
+  const GridSlot gs = grid_slot(blockIdx.x, nbh, nqb, chunk);
+  const int bh = gs.pair;
+  const int qb = CAUSAL ? nqb - 1 - gs.rank : gs.rank;  // causal: the longest query rows first
   const int b = bh / p.heads, h = bh % p.heads;
   const int hk = h / (p.heads / p.kv_heads);
   const long rs = (long)p.heads * D;      // query-side row stride
@@ -187,7 +187,9 @@ fwd_kernel(FwdParams<T> p) {
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_fwd(const FwdParams<T>& p, hipStream_t stream) {
   const int nqb = (p.nq + 32 * kWaves - 1) / (32 * kWaves);
-  hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL>), dim3(nqb * p.batch * p.heads), dim3(kThreads), 0, stream, p);
+  const int npairs = p.batch * p.heads;
+  const int chunk = grid_chunk(npairs, nqb, resident_workgroups(Occupancy<T, D>::value));
+  hipLaunchKernelGGL((fwd_kernel<T, D, CAUSAL>), dim3(nqb * npairs), dim3(kThreads), 0, stream, p, chunk);
   return hipGetLastError();
 }
 

@@ -92,3 +92,38 @@ def test_repeat_and_shard_bit_exact(case):
             f"head shard {hk}: dK2/dV2"
         for s, rs in zip(stats, rstats):
             assert torch.equal(s, rs[:, hs]), f"head shard {hk}: row statistics"
+
+
+# Grids of more than 8 rounds of resident workgroups (256 CUs, two workgroups
+# per CU) take the (batch, head) pairs in chunks, the last chunk short here;
+# a one-sample call takes the plain order. Each workgroup's arithmetic does not
+# depend on its place in the grid, so every sample of the large call equals its
+# own one-sample call bit for bit: forward, first backward and double backward.
+LARGE = [
+    # name, B, N, H, H_kv, dtype, causal
+    ("bf16_causal_b130", 130, 512, 16, 16, torch.bfloat16, 1),
+    ("f16_gqa_noncausal_ragged_b140", 140, 300, 8, 2, torch.float16, 0),
+]
+
+
+def _run_all(x, causal, scale):
+    from flash_hog import _hip
+
+    out = _run(x, causal, scale)
+    o, lse = out[0], out[1]
+    return out + tuple(_hip.attention_bwd(x["q"], x["k"], x["v"], o, x["do"], lse, causal, scale))
+
+
+@pytest.mark.parametrize("case", LARGE, ids=[c[0] for c in LARGE])
+def test_chunked_grid_equals_per_sample(case):
+    name, B, N, H, Hkv, dtype, causal = case
+    _announce("grid order", name, B, N, H, Hkv)
+    dev = torch.device("cuda:0")
+    D = 64
+    scale = 1.0 / math.sqrt(D)
+    x = make_inputs(B, N, N, H, D, dtype, seed=11, device=dev, kv_heads=Hkv)
+    ref = _run_all(x, causal, scale)
+    for b in range(B):
+        part = _run_all(_slice(x, b=slice(b, b + 1)), causal, scale)
+        for i, (a, r) in enumerate(zip(part, ref)):
+            assert torch.equal(a, r[b:b + 1]), f"sample {b}, output {i}"
