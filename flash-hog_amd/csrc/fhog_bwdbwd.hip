@@ -391,44 +391,11 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
     }
 
     if (qt_begin < nqt) {
-      // Key-side operands (B of the score products).
-      V8<T> kf[KS], dkf[KS], vf[KS], dvf[KS];
-  #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const long off = kbase + (long)kj * rsk + 16 * ks + 8 * g;
-        if (kvalid) {
-          kf[ks] = *reinterpret_cast<const V8<T>*>(p.k + off);
-          dkf[ks] = *reinterpret_cast<const V8<T>*>(p.ddk + off);
-          vf[ks] = *reinterpret_cast<const V8<T>*>(p.v + off);
-          dvf[ks] = *reinterpret_cast<const V8<T>*>(p.ddv + off);
-        } else {
-          kf[ks] = zero8<T>();
-          dkf[ks] = zero8<T>();
-          vf[ks] = zero8<T>();
-          dvf[ks] = zero8<T>();
-        }
-      }
       const float scale = p.scale;
-      if constexpr (PRE) {
-        // scale is a power of two: K and ddK carry it exactly, so S and ddS come
-        // out of the matrix products already scaled (bit-identical to scaling
-        // them afterwards) and the element-wise step skips one multiply.
-  #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-  #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            kf[ks][e] = (T)((float)kf[ks][e] * scale);
-            dkf[ks][e] = (T)((float)dkf[ks][e] * scale);
-          }
-      }
-      const float c2 = PRE ? kLog2e : scale * kLog2e;
-
       SwzFrags<T, D> fr;
       fr.init(lane);
 
       const int total = (nqt - qt_begin) * grp;
-      // Retire the key-side loads before the ring starts (see bwdbwd_q_kernel).
-      wait_vmem();
       const T* src = (wave == 0 ? p.q : wave == 1 ? p.dout : p.ddq) + qbase;
       const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
       TileDma<T, D> dma;
@@ -502,6 +469,8 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
         gnext += c.gi + 1 == grp ? row_step : (long)D;
         c.next(grp);
       };
+      // The ring's first tiles go out before the key-side loads, so that both
+      // latencies overlap (this also shortens the loads' live ranges).
       GroupCursor nxt;  // iteration of the next tile to issue
   #pragma unroll
       for (int i = 0; i < NST - 1; ++i)
@@ -509,6 +478,42 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
           issue(i, nxt);
           advance(nxt);
         }
+
+      // Key-side operands (B of the score products).
+      V8<T> kf[KS], dkf[KS], vf[KS], dvf[KS];
+  #pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const long off = kbase + (long)kj * rsk + 16 * ks + 8 * g;
+        if (kvalid) {
+          kf[ks] = *reinterpret_cast<const V8<T>*>(p.k + off);
+          dkf[ks] = *reinterpret_cast<const V8<T>*>(p.ddk + off);
+          vf[ks] = *reinterpret_cast<const V8<T>*>(p.v + off);
+          dvf[ks] = *reinterpret_cast<const V8<T>*>(p.ddv + off);
+        } else {
+          kf[ks] = zero8<T>();
+          dkf[ks] = zero8<T>();
+          vf[ks] = zero8<T>();
+          dvf[ks] = zero8<T>();
+        }
+      }
+      if constexpr (PRE) {
+        // scale is a power of two: K and ddK carry it exactly, so S and ddS come
+        // out of the matrix products already scaled (bit-identical to scaling
+        // them afterwards) and the element-wise step skips one multiply.
+  #pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            kf[ks][e] = (T)((float)kf[ks][e] * scale);
+            dkf[ks][e] = (T)((float)dkf[ks][e] * scale);
+          }
+      }
+      const float c2 = PRE ? kLog2e : scale * kLog2e;
+
+      // Retire the key-side loads (and with them the first tiles) before the
+      // loop: vmcnt counts the untracked LDS DMAs too, so a wait for the loads
+      // inside the loop would drain the prefetched tiles.
+      wait_vmem();
       if (wave == 3) {
         wait_stats(0);
         finish_stats(0);
