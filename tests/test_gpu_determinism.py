@@ -8,7 +8,9 @@ workgroups from its own inputs. Hence, bit for bit:
 - the batch can be split into shards (each shard a separate call) and the
   shards' outputs equal the corresponding slices of the unsplit call;
 - heads can be split the same way, in whole key/value-head groups for grouped
-  queries (query head h reads key/value head h / (H / H_kv)).
+  queries (query head h reads key/value head h / (H / H_kv));
+- the order in which a grid takes its blocks (plain or in chunks of
+  (batch, head) pairs, chosen from the grid's size) does not change any output.
 
 The last two are the sharding over (B, H) that needs no exchange between
 devices (the reference's multi-device test shards the batch,
