@@ -103,7 +103,8 @@ fwd_kernel(FwdParams<T> p, int chunk) {
   };
 
   const float c2 = p.scale * kLog2e;
-  float m = -1e30f;  // running row max of the log2-domain logits
+  constexpr float kRescale = 8.f;
+  float m = -1e30f;  // running row max of the log2-domain logits (possibly stale, see below)
   float lpart = 0.f; // this lane's share of the running row sum
   f32x16 acc[DT];
 #pragma unroll
@@ -139,7 +140,11 @@ fwd_kernel(FwdParams<T> p, int chunk) {
 #pragma unroll
       for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, S[r]);
       const float mnew = fmaxf(m, xgroup_max(mloc));
-      if (__any(mnew != m)) {
+      // Lazy rescale: a row keeps its running maximum until it grows by more
+      // than kRescale (log2 units), so P <= 2^kRescale and O, l carry the same
+      // stale factor, which the final O / l and L = m + log2 l cancel. Most
+      // tiles then skip the exp and the 33 multiplies of a rescale.
+      if (__any(mnew > m + kRescale)) {
         const float alpha = exp2_fast(m - mnew);
         lpart *= alpha;
 #pragma unroll
