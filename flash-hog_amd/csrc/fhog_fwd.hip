@@ -127,8 +127,9 @@ fwd_kernel(FwdParams<T> p, int chunk) {
       f32x16 S = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) S = mma<T>(fr.rowf(sa, 0, ks), qf[ks], S);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) S[r] *= c2;
+      // S stays unscaled: the row maximum is taken on it and scaled once
+      // (c2 > 0, and rounding is monotonic, so this equals the maximum of the
+      // scaled values), and the scale enters the exponent's fma below.
       const int k0 = kt * BK;
       if ((k0 + BK > p.nk) || (CAUSAL && k0 + BK - 1 > q0 + p.coff)) {
         const int klim = min(p.nk - 1, CAUSAL ? qi + p.coff : p.nk - 1) - k0;  // last visible key, tile-relative
@@ -139,7 +140,7 @@ fwd_kernel(FwdParams<T> p, int chunk) {
       float mloc = S[0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, S[r]);
-      const float mnew = fmaxf(m, xgroup_max(mloc));
+      const float mnew = fmaxf(m, xgroup_max(mloc * c2));
       // Lazy rescale: a row keeps its running maximum until it grows by more
       // than kRescale (log2 units), so P <= 2^kRescale and O, l carry the same
       // stale factor, which the final O / l and L = m + log2 l cancel. Most
@@ -154,7 +155,7 @@ fwd_kernel(FwdParams<T> p, int chunk) {
       float psum = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        S[r] = exp2_fast(S[r] - m);  // masked: exp2(-inf) = 0
+        S[r] = exp2_fast(fmaf(S[r], c2, -m));  // masked: exp2(-inf) = 0
         psum += S[r];
       }
       lpart += psum;
