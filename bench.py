@@ -103,6 +103,20 @@ def stage1_traffic():
     return {"bytes": int(fetch + write), "source": TRAFFIC_FILE.name}
 
 
+def available_cores():
+    """CPUs this process may use: its affinity mask, capped by the cgroup CPU
+    quota (cpu.max, cgroup v2) when one is set, since a container can see more
+    CPUs than its quota lets it run at once."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, math.ceil(int(quota) / int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
 def cpu_baseline(args, B, N, H, D, scale, causal):
     """The reference's CPU path restated: torch-CPU fp32 autograd double VJP of
     materialised attention (oracle/autodiff.py), one (batch, head) slice at a
@@ -111,7 +125,7 @@ def cpu_baseline(args, B, N, H, D, scale, causal):
 
     from oracle import autodiff
 
-    cores = min(len(os.sched_getaffinity(0)), args.cpu_threads)
+    cores = args.cpu_threads or available_cores()
     torch.set_num_threads(cores)
     names = ("q", "k", "v", "do", "ddq", "ddk", "ddv")
 
@@ -366,7 +380,8 @@ def main(argv=None):
                     help="run the workload untimed for this long before the warm-up steps (clock ramp)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads of the CPU baseline (default: every core available to the process)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one device copy of this many MiB first (PMC byte-counter calibration)")
     ap.add_argument("--configs", action="store_true",
@@ -464,9 +479,9 @@ def main(argv=None):
     value = alg_flops / (ms_per_step * 1e-3) / 1e12
     s1_alg = 18.0 * D * pairs
     s1_tflops = s1_alg / (s1_ms * 1e-3) / 1e12
-    # executed MFMA work per unmasked pair: stage 1 = 12 products (5 score and
-    # 7 output products in one sweep), stage 2 = 8 products; 2 * d flops each
-    exec_tflops = (24.0 + 16.0) * D * pairs / (ms_per_step * 1e-3) / 1e12
+    # executed MFMA work per unmasked pair: stage 1 = 11 products (5 score and
+    # 6 output products in one sweep), stage 2 = 8 products; 2 * d flops each
+    exec_tflops = (22.0 + 16.0) * D * pairs / (ms_per_step * 1e-3) / 1e12
     traffic = stage1_traffic()
 
     # Peak memory of one call with torch-owned outputs, against the inputs.

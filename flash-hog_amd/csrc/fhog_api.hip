@@ -42,6 +42,9 @@ struct Shape {
 int check_shape(const Shape& s, const char* who) {
   if (!(s.scale == s.scale) || s.scale - s.scale != 0.0f)
     return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: scale must be finite", who);
+  // With scale 0 every logit is 0 and masked ones are -inf * 0; the kernels
+  // also divide by the scale. Any other finite scale, negative included, works.
+  if (s.scale == 0.0f) return fail(FHOG_ERR_UNSUPPORTED, "%s: scale must be nonzero", who);
   if (s.causal != FHOG_CAUSAL_NONE && s.causal != FHOG_CAUSAL_TOP_LEFT && s.causal != FHOG_CAUSAL_BOTTOM_RIGHT)
     return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: causal must be 0 (none), 1 (top-left) or 2 (bottom-right), got %d",
                 who, s.causal);

@@ -230,30 +230,36 @@ struct GroupCursor {
 // explicit vmcnt wait and a workgroup barrier before a staged tile is read, a
 // barrier before a stage is overwritten. Untracked vector-memory operations
 // only make the compiler's own vmcnt waits more conservative, never less.
+//
+// The LDS destination goes in M0. It is an operand bound to that register
+// ("{m0}"), so the compiler itself writes M0 before the statement and knows
+// its value afterwards; the statement only reads M0. The s_nop is the one wait
+// state the hardware needs between an SALU write of M0 and an LDS DMA, which
+// the compiler's hazard check does not see inside inline assembly.
 
 // 16 bytes per lane, addressed as a uniform 64-bit base (SGPR pair) plus a
 // per-lane 32-bit byte offset.
 __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(voff), "s"(sbase), "s"(lds_byte_addr)
-               : "memory", "m0");
+               : "v"(voff), "s"(sbase), "{m0}"(lds_byte_addr)
+               : "memory");
 }
 
 // 4 bytes per lane from a per-lane 64-bit address.
 __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_byte_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off"
                :
-               : "v"(gptr), "s"(lds_byte_addr)
-               : "memory", "m0");
+               : "v"(gptr), "{m0}"(lds_byte_addr)
+               : "memory");
 }
 
 // 4 bytes per lane, addressed as a uniform base plus a per-lane byte offset.
 __device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
                :
-               : "v"(voff), "s"(sbase), "s"(lds_byte_addr)
-               : "memory", "m0");
+               : "v"(voff), "s"(sbase), "{m0}"(lds_byte_addr)
+               : "memory");
 }
 
 // Per-lane source offsets of the wave-wide loads that fill one swizzled 32 x D

@@ -63,11 +63,15 @@ fwd_kernel(FwdParams<T> p, int chunk) {
   const int qi = q0 + n;
   const bool qvalid = qi < p.nq;
 
+  // A negative scale is applied as |scale| to -Q (negation is exact), so the
+  // logits the running maximum is taken over are the unscaled scores of -Q.
+  const bool negate = p.scale < 0.f;
   V8<T> qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const long off = qbase + (long)qi * rs + 16 * ks + 8 * g;
     qf[ks] = qvalid ? *reinterpret_cast<const V8<T>*>(p.q + off) : zero8<T>();
+    if (negate) qf[ks] = -qf[ks];
   }
 
   // Keys [0, kend) are visible to some query of the workgroup, [0, wend) to
@@ -102,7 +106,7 @@ fwd_kernel(FwdParams<T> p, int chunk) {
     }
   };
 
-  const float c2 = p.scale * kLog2e;
+  const float c2 = fabsf(p.scale) * kLog2e;  // > 0
   constexpr float kRescale = 8.f;
   float m = -1e30f;  // running row max of the log2-domain logits (possibly stale, see below)
   float lpart = 0.f; // this lane's share of the running row sum

@@ -1,10 +1,12 @@
-"""fp32 closed-form double backward on the GPU, one head at a time.
+"""fp32 closed-form attention forward, first and double backward on the GPU,
+one head at a time.
 
 A checker for the full-size configurations, where the numpy fp64 oracle would
-take minutes: the same equations as oracle/attention.py:bwd_bwd_head
-(flash_hog/_jax_refs/jax_impl.py:301-336), materialising (N_Q, N_K) fp32
-matrices for one (batch, head) at a time. It is pinned against the fp64 oracle
-in tests/test_gpu_parity.py::test_gpu_reference_matches_oracle.
+take minutes: the same equations as oracle/attention.py (attn_fwd, attn_bwd,
+bwd_bwd_head; flash_hog/_jax_refs/jax_impl.py:112-191, 301-336),
+materialising (N_Q, N_K) fp32 matrices for one (batch, head) at a time. Each
+function is pinned against the fp64 oracle in
+tests/test_gpu_parity.py::test_gpu_reference_matches_oracle.
 """
 
 from __future__ import annotations
@@ -46,6 +48,33 @@ def fwd_head(q, k, v, scale, causal):
     return torch.mm(torch.exp(s - lse[:, None]), v), lse
 
 
+def bwd_head(q, k, v, o, do, lse, scale, causal):
+    """First backward (flash_hog/_jax_refs/jax_impl.py:142-191): dQ, dK, dV and D = rowsum(O dO)."""
+    mm = torch.mm
+    s = mm(q, k.t().contiguous()) * scale
+    if causal:
+        s = s.masked_fill(~_mask(q.shape[0], k.shape[0], q.device), float("-inf"))
+    p = torch.exp(s - lse[:, None])
+    dp = mm(do, v.t().contiguous())
+    d = (o * do).sum(-1)
+    ds = scale * p * (dp - d[:, None])
+    return mm(ds, k), mm(ds.t().contiguous(), q), mm(p.t().contiguous(), do), d
+
+
+def bwd(q, k, v, o, do, lse, scale, causal, heads=None):
+    """(B, T, N, H) inputs -> fp32 dQ, dK, dV (B, T, N, H) and D (B, N, T) on the
+    listed (batch, head) pairs (default: all); other entries are zero."""
+    f = lambda x: x.float()
+    q, k, v, o, do, lse = map(f, (q, k, v, o, do, lse))
+    B, T, H, _ = q.shape
+    outs = [torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v), torch.zeros((B, H, T), device=q.device)]
+    for b, h in heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]:
+        args = [x[b, :, h, :].contiguous() for x in (q, k, v, o, do)]
+        dq, dk, dv, d = bwd_head(*args, lse[b, h].contiguous(), scale, causal)
+        outs[0][b, :, h, :], outs[1][b, :, h, :], outs[2][b, :, h, :], outs[3][b, h] = dq, dk, dv, d
+    return tuple(outs)
+
+
 def bwdbwd(q, k, v, o, do, ddq, ddk, ddv, lse, scale, causal):
     """(B, T, N, H) inputs of any float dtype -> fp32 dQ2, dK2, dV2, ddO."""
     f = lambda x: x.float()
@@ -61,13 +90,14 @@ def bwdbwd(q, k, v, o, do, ddq, ddk, ddv, lse, scale, causal):
     return tuple(outs)
 
 
-def fwd(q, k, v, scale, causal):
+def fwd(q, k, v, scale, causal, heads=None):
+    """(B, T, N, H) inputs -> fp32 O (B, T, N, H) and natural-log L (B, N, T) on
+    the listed (batch, head) pairs (default: all); other entries are zero."""
     q, k, v = q.float(), k.float(), v.float()
     B, T, H, D = q.shape
-    o = torch.empty((B, T, H, v.shape[-1]), device=q.device)
-    lse = torch.empty((B, H, T), device=q.device)
-    for b in range(B):
-        for h in range(H):
-            o[b, :, h, :], lse[b, h] = fwd_head(q[b, :, h, :].contiguous(), k[b, :, h, :].contiguous(),
-                                                v[b, :, h, :].contiguous(), scale, causal)
+    o = torch.zeros((B, T, H, v.shape[-1]), device=q.device)
+    lse = torch.zeros((B, H, T), device=q.device)
+    for b, h in heads if heads is not None else [(b, h) for b in range(B) for h in range(H)]:
+        o[b, :, h, :], lse[b, h] = fwd_head(q[b, :, h, :].contiguous(), k[b, :, h, :].contiguous(),
+                                            v[b, :, h, :].contiguous(), scale, causal)
     return o, lse

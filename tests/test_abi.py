@@ -77,6 +77,9 @@ def _bwdbwd_args(ptr=16, batch=1, n_q=16, n_k=16, heads=1, kv_heads=1, head_dim=
     (dict(head_dim=96), 2, "head_dim must be 64 or 128"),
     (dict(head_dim=128, dtype=0), 2, "fp32 supports head_dim 64"),
     (dict(scale=float("nan")), 1, "scale"),
+    (dict(scale=float("inf")), 1, "scale must be finite"),
+    (dict(scale=0.0), 2, "scale must be nonzero"),
+    (dict(scale=-0.0), 2, "scale must be nonzero"),
 ])
 def test_bwdbwd_rejects_invalid_arguments(lib, kwargs, status, needle):
     st = lib.fhog_attention_bwdbwd(*_bwdbwd_args(**kwargs))

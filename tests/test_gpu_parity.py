@@ -50,6 +50,22 @@ CASES = [
 ]
 IDS = [c[0] for c in CASES]
 
+# Softmax scales other than the default 1/sqrt(D) (id, batch, n_q, n_k, heads,
+# kv_heads, head_dim, dtype, causal, scale). Only a positive power-of-two scale
+# lets the bf16 D = 64 kernels fold it into the resident operands; these cases
+# run the general instances, and negative scales (the forward then takes its
+# running maximum over the scaled logits' other end).
+SCALE_CASES = [
+    ("bf16_causal_scale_0.1", 2, 256, 256, 2, 2, 64, BF16, TL, 0.1),
+    ("bf16_noncausal_ragged_scale_0.3", 1, 200, 200, 2, 2, 64, BF16, NONE, 0.3),
+    ("bf16_causal_scale_-0.1", 1, 256, 256, 2, 2, 64, BF16, TL, -0.1),
+    ("bf16_causal_scale_-0.125", 1, 192, 192, 2, 2, 64, BF16, TL, -0.125),
+    ("f16_noncausal_ragged_scale_-0.2", 1, 150, 150, 2, 2, 64, F16, NONE, -0.2),
+    ("f16_d128_bottom_right_scale_-0.05", 1, 100, 160, 2, 1, 128, F16, BR, -0.05),
+    ("f32_causal_scale_-0.125", 1, 96, 96, 2, 2, 64, F32, TL, -0.125),
+]
+SCALE_IDS = [c[0] for c in SCALE_CASES]
+
 
 def _lse_err(lse, lse_ref):
     """max |L - L_ref| over rows that see a key, relative to max(1, |L_ref|);
@@ -132,6 +148,43 @@ def test_bwdbwd_matches_oracle(case, cuda_device):
         assert torch.isfinite(torch.as_tensor(a)).all(), label
 
 
+@pytest.mark.parametrize("case", SCALE_CASES, ids=SCALE_IDS)
+def test_all_kernels_other_scales(case, cuda_device):
+    """Forward, first backward and double backward against the oracle at
+    non-default and negative softmax scales."""
+    name, B, Nq, Nk, H, Hk, D, dtype, causal, scale = case
+    _announce("scale", name)
+    from flash_hog import _hip
+
+    x = make_inputs(B, Nq, Nk, H, D, dtype, seed=53, kv_heads=Hk)
+    g = lambda t: t.to(cuda_device)
+    o_k, lse_k = _hip.attention_fwd(g(x["q"]), g(x["k"]), g(x["v"]), causal, scale)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = ora.attn_fwd(to_np(x["q"]), to_np(x["k"]), to_np(x["v"]), scale, causal)
+    assert rel_err(o_k, o_ref, DEGENERATE_FLOOR) < TOL[dtype], "O"
+    assert _lse_err(lse_k, lse_ref) < 1e-3, "L"
+
+    o, lse = _oracle_residual(x, scale, causal, dtype)
+    got = _hip.attention_bwd(g(x["q"]), g(x["k"]), g(x["v"]), g(o), g(x["do"]), g(lse), causal, scale)
+    torch.cuda.synchronize()
+    ref = ora.attn_bwd(to_np(x["q"]), to_np(x["k"]), to_np(x["v"]), to_np(o), to_np(x["do"]), to_np(lse),
+                       scale, causal)
+    for a, r, label in zip(got, ref, ("dq", "dk", "dv", "D")):
+        err = rel_err(a, r, DEGENERATE_FLOOR)
+        assert err < TOL[dtype], f"{label}: rel err {err:.3e}"
+
+    dq2, dk2, dv2, ddo, stats = _hip.attention_bwdbwd(
+        g(x["q"]), g(x["k"]), g(x["v"]), g(o), g(x["do"]), g(x["ddq"]), g(x["ddk"]), g(x["ddv"]), g(lse),
+        causal, scale, return_stats=True)
+    torch.cuda.synchronize()
+    ref = ora.attn_bwd_bwd_stats(*(to_np(x[n]) for n in ("q", "k", "v")), to_np(o), to_np(x["do"]),
+                                 *(to_np(x[n]) for n in ("ddq", "ddk", "ddv")), to_np(lse), scale, causal,
+                                 return_stats=True)
+    for a, r, label in zip((dq2, dk2, dv2, ddo) + tuple(stats), ref, ("dq2", "dk2", "dv2", "ddo", "D", "dD", "B")):
+        err = rel_err(a, r, DEGENERATE_FLOOR)
+        assert err < TOL[dtype], f"{label}: rel err {err:.3e}"
+
+
 def _golden():
     import pathlib
 
@@ -159,7 +212,8 @@ def test_bwdbwd_golden_vectors(dtype, cuda_device):
 
 
 def test_gpu_reference_matches_oracle(cuda_device):
-    """Pins the fp32 GPU checker used at full size against the fp64 oracle."""
+    """Pins the fp32 GPU checkers used at full size (forward, first backward,
+    double backward) against the fp64 oracle."""
     import gpu_reference
 
     _announce("gpu_reference pin")
@@ -167,6 +221,15 @@ def test_gpu_reference_matches_oracle(cuda_device):
     scale = default_scale(64)
     o, lse = _oracle_residual(x, scale, True, F32)
     g = lambda t: t.to(cuda_device)
+    o_g, l_g = gpu_reference.fwd(g(x["q"]), g(x["k"]), g(x["v"]), scale, True)
+    o_r, l_r = ora.attn_fwd(to_np(x["q"]), to_np(x["k"]), to_np(x["v"]), scale, True)
+    assert rel_err(o_g, o_r) < 1e-4
+    assert _lse_err(l_g, l_r) < 1e-5
+    got = gpu_reference.bwd(g(x["q"]), g(x["k"]), g(x["v"]), g(o), g(x["do"]), g(lse), scale, True)
+    ref = ora.attn_bwd(to_np(x["q"]), to_np(x["k"]), to_np(x["v"]), to_np(o), to_np(x["do"]), to_np(lse),
+                       scale, True)
+    for a, r in zip(got, ref):
+        assert rel_err(a, r) < 1e-4
     got = gpu_reference.bwdbwd(*(g(x[n]) for n in ("q", "k", "v")), g(o), g(x["do"]),
                                *(g(x[n]) for n in ("ddq", "ddk", "ddv")), g(lse), scale, True)
     ref = ora.attn_bwd_bwd_stats(*(to_np(x[n]) for n in ("q", "k", "v")), to_np(o), to_np(x["do"]),
