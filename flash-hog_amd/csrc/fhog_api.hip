@@ -7,6 +7,9 @@
 #include <stdio.h>
 #include <stdarg.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "flash_hog.h"
 #include "fhog_params.h"
 
@@ -105,7 +108,7 @@ hipError_t dispatch(int dtype, int head_dim, bool causal, F&& f) {
 
 extern "C" {
 
-int fhog_abi_version(void) { return 101; }
+int fhog_abi_version(void) { return 102; }
 
 const char* fhog_status_string(int status) {
   switch (status) {
@@ -185,6 +188,53 @@ int bwdbwd_impl(const char* who, int stages, fhog_stream_t stream, const void* q
   return launch_status(dispatch(dtype, head_dim, causal != 0, run), who);
 }
 
+// ---------------------------------------------------------------------------
+// Row statistics of fhog_attention_bwdbwd_noalloc: D, dD and B of up to
+// kScratchRows (batch, head, query) rows each, in one file-scope device array
+// (12 MiB per device, held until the process ends). Every call on a device
+// uses that device's copy; the kernels write every row they later read, so
+// nothing needs clearing between calls, but two calls that overlap on one
+// device race on it.
+// ---------------------------------------------------------------------------
+constexpr long long kScratchRows = 1ll << 20;
+static __device__ __align__(256) float scratch[3 * kScratchRows];
+
+// Device address of `scratch` per device, looked up once per device (with
+// that device current) and kept: in host code the array's name is not a
+// device address.
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int scratch_address(const char* who, hipStream_t stream, float** out) {
+  int dev = -1;
+  hipError_t e = stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FHOG_ERR_LAUNCH, "%s: cannot find the stream's device: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(FHOG_ERR_UNSUPPORTED, "%s: device %d out of range", who, dev);
+  float* ptr = g_scratch[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      int cur = -1;
+      if ((e = hipGetDevice(&cur)) == hipSuccess && cur != dev) e = hipSetDevice(dev);
+      void* addr = nullptr;
+      if (e == hipSuccess) e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (cur >= 0 && cur != dev) {
+        const hipError_t back = hipSetDevice(cur);
+        if (e == hipSuccess) e = back;
+      }
+      if (e != hipSuccess || addr == nullptr)
+        return fail(FHOG_ERR_LAUNCH, "%s: no address for the static scratch on device %d: %s", who, dev,
+                    hipGetErrorString(e));
+      ptr = static_cast<float*>(addr);
+      g_scratch[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return FHOG_OK;
+}
+
 }  // namespace
 
 int fhog_attention_bwdbwd(fhog_stream_t stream, const void* q, const void* k, const void* v, const void* o,
@@ -205,6 +255,32 @@ int fhog_attention_bwdbwd_stage(fhog_stream_t stream, int stage, const void* q, 
   if (stage != 1 && stage != 2) return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: stage must be 1 or 2, got %d", who, stage);
   return bwdbwd_impl(who, stage, stream, q, k, v, o, dout, ddq, ddk, ddv, lse, dq2, dk2, dv2, ddo, delta,
                      ddelta, bstat, batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal, scale);
+}
+
+int fhog_attention_bwdbwd_noalloc(fhog_stream_t stream, const void* q, const void* k, const void* v,
+                                  const void* o, const void* dout, const void* ddq, const void* ddk,
+                                  const void* ddv, const float* lse, void* dq2, void* dk2, void* dv2, void* ddo,
+                                  int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim, int dtype,
+                                  int causal, float scale) {
+  static const char* who = "fhog_attention_bwdbwd_noalloc";
+  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal, scale};
+  if (int st = check_shape(s, who)) return st;
+  if (int st = check_ptrs(who, {{"q", q}, {"k", k}, {"v", v}, {"o", o}, {"dout", dout}, {"ddq", ddq},
+                                {"ddk", ddk}, {"ddv", ddv}, {"dq2", dq2}, {"dk2", dk2}, {"dv2", dv2},
+                                {"ddo", ddo}},
+                           {{"lse", lse}}))
+    return st;
+  const long long rows = (long long)batch * heads * n_q;
+  if (rows > kScratchRows)
+    return fail(FHOG_ERR_UNSUPPORTED,
+                "%s: batch * heads * n_q = %lld exceeds the static scratch's %lld rows; use fhog_attention_bwdbwd "
+                "with caller-owned row statistics",
+                who, rows, kScratchRows);
+  float* ws = nullptr;
+  if (int st = scratch_address(who, (hipStream_t)stream, &ws)) return st;
+  return bwdbwd_impl(who, 3, stream, q, k, v, o, dout, ddq, ddk, ddv, lse, dq2, dk2, dv2, ddo, ws,
+                     ws + kScratchRows, ws + 2 * kScratchRows, batch, n_q, n_k, heads, kv_heads, head_dim, dtype,
+                     causal, scale);
 }
 
 }  // extern "C"

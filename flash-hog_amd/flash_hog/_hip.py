@@ -44,6 +44,7 @@ SIGNATURES = {
     "fhog_attention_bwd": (_i, [_p] * 11 + [_i] * 8 + [_f]),
     "fhog_attention_bwdbwd": (_i, [_p] * 17 + [_i] * 8 + [_f]),
     "fhog_attention_bwdbwd_stage": (_i, [_p, _i] + [_p] * 16 + [_i] * 8 + [_f]),
+    "fhog_attention_bwdbwd_noalloc": (_i, [_p] * 14 + [_i] * 8 + [_f]),
 }
 
 
@@ -195,4 +196,37 @@ def attention_bwdbwd(q, k, v, o, dout, ddq, ddk, ddv, lse, causal, scale: float,
             B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], causal_code(causal), float(scale)))
     if return_stats:
         return dq2, dk2, dv2, ddo, (stats[0], stats[1], stats[2])
+    return dq2, dk2, dv2, ddo
+
+
+def attention_bwdbwd_noalloc(q, k, v, o, dout, ddq, ddk, ddv, lse, causal, scale: float, out=None):
+    """attention_bwdbwd through fhog_attention_bwdbwd_noalloc: the row
+    statistics live in the library's static device scratch, so the call needs
+    no workspace. `out` = (dq2, dk2, dv2, ddo) preallocated outputs (allocated
+    here when None)."""
+    _check_inputs([("q", q), ("k", k), ("v", v), ("o", o), ("dout", dout),
+                   ("ddq", ddq), ("ddk", ddk), ("ddv", ddv)], q.dtype)
+    _check_inputs([("q", q), ("lse", lse)])
+    B, Tq, Tk, N, Nk, Hd = _dims(q, k)
+    _expect("v", v, k.shape)
+    for name, t in (("o", o), ("dout", dout), ("ddq", ddq)):
+        _expect(name, t, q.shape)
+    for name, t in (("ddk", ddk), ("ddv", ddv)):
+        _expect(name, t, k.shape)
+    _expect("lse", lse, (B, N, Tq), torch.float32)
+    q, k, v, o, dout, ddq, ddk, ddv, lse = (
+        x.contiguous() for x in (q, k, v, o, dout, ddq, ddk, ddv, lse))
+    if out is None:
+        out = tuple(torch.empty_like(x) for x in (q, k, v, dout))
+    for name, t, like in zip(("dq2", "dk2", "dv2", "ddo"), out, (q, k, v, dout)):
+        _expect(name, t, like.shape, like.dtype)
+        if not t.is_contiguous() or t.device != q.device:
+            raise ValueError(f"{name} must be contiguous on {q.device}")
+    dq2, dk2, dv2, ddo = out
+    with torch.cuda.device(q.device):
+        check(lib().fhog_attention_bwdbwd_noalloc(
+            _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(dout),
+            _ptr(ddq), _ptr(ddk), _ptr(ddv), _ptr(lse),
+            _ptr(dq2), _ptr(dk2), _ptr(dv2), _ptr(ddo),
+            B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], causal_code(causal), float(scale)))
     return dq2, dk2, dv2, ddo

@@ -5,8 +5,9 @@
  * given HIP stream and returns without synchronising; it allocates nothing,
  * frees nothing and keeps no pointer after it returns (all outputs and the
  * fp32 row-statistic workspace are caller owned, as the reference's XLA FFI
- * handler exposes its dD/B scratch as results). No entry point holds mutable
- * global state, so concurrent calls on different streams are safe.
+ * handler exposes its dD/B scratch as results). No entry point except
+ * fhog_attention_bwdbwd_noalloc holds mutable global state, so concurrent
+ * calls on different streams are safe.
  *
  * Layouts (identical to the reference's attention seam):
  *   q, o, dout, ddq, dq, dq2, ddo   : (batch, n_q, heads, head_dim) contiguous
@@ -142,6 +143,28 @@ int fhog_attention_bwdbwd_stage(fhog_stream_t stream, int stage,
                                 float* delta, float* ddelta, float* bstat,
                                 int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim,
                                 int dtype, int causal, float scale);
+
+/*
+ * fhog_attention_bwdbwd without the row-statistic workspace arguments: D, dD
+ * and B go to a static device array inside the library (12 MiB per device,
+ * for batch * heads * n_q up to 1048576 rows; larger calls return
+ * FHOG_ERR_UNSUPPORTED). Outputs are those of fhog_attention_bwdbwd, bit for
+ * bit. It calls no allocating routine, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses
+ * that forbid hipMalloc); the first call on a device looks up the array's
+ * address there once. It has no counterpart in the reference, whose handler
+ * receives its scratch from XLA (ffi.cu:79-98). Every call on a device shares
+ * that device's array: calls that overlap on one device (concurrent streams)
+ * race on it and must be serialised by the caller.
+ */
+int fhog_attention_bwdbwd_noalloc(fhog_stream_t stream,
+                                  const void* q, const void* k, const void* v,
+                                  const void* o, const void* dout,
+                                  const void* ddq, const void* ddk, const void* ddv,
+                                  const float* lse,
+                                  void* dq2, void* dk2, void* dv2, void* ddo,
+                                  int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim,
+                                  int dtype, int causal, float scale);
 
 #ifdef __cplusplus
 }

@@ -47,7 +47,7 @@ def test_python_signatures_cover_the_header():
 
 
 def test_status_strings(lib):
-    assert lib.fhog_abi_version() == 101
+    assert lib.fhog_abi_version() == 102
     assert lib.fhog_status_string(0) == b"ok"
     assert lib.fhog_status_string(1) == b"invalid argument"
     assert lib.fhog_status_string(2) == b"unsupported"
@@ -121,3 +121,41 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     finally:
         monkeypatch.delenv(_hip.LIB_ENV)
         _hip.lib.cache_clear()
+
+
+def _noalloc_args(ptr=16, batch=1, n_q=16, n_k=16, heads=1, kv_heads=1, head_dim=64, dtype=2, causal=1,
+                  scale=0.125):
+    return [None] + [ptr] * 13 + [batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal, scale]
+
+
+@pytest.mark.parametrize("kwargs,status,needle", [
+    (dict(ptr=None), 1, "q is null"),
+    (dict(ptr=8), 1, "not 16-byte aligned"),
+    (dict(scale=0.0), 2, "scale must be nonzero"),
+    (dict(head_dim=96), 2, "head_dim must be 64 or 128"),
+    # 1048577 (batch, head, query) rows: one more than the static scratch holds
+    (dict(batch=1, heads=1, kv_heads=1, n_q=(1 << 20) + 1, n_k=64), 2, "exceeds the static scratch"),
+    (dict(batch=64, heads=16, kv_heads=16, n_q=1025, n_k=1025), 2, "exceeds the static scratch"),
+])
+def test_bwdbwd_noalloc_rejects_before_touching_the_gpu(lib, kwargs, status, needle):
+    st = lib.fhog_attention_bwdbwd_noalloc(*_noalloc_args(**kwargs))
+    assert st == status
+    assert needle in lib.fhog_last_error().decode()
+
+
+def test_library_imports_no_allocating_hip_routine():
+    """No entry point allocates or frees device or host memory through HIP."""
+    import shutil
+    import subprocess
+
+    from flash_hog import _hip
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--undefined-only", str(_hip.library_path())], capture_output=True,
+                         text=True, check=True).stdout
+    imported = set(re.findall(r"\b(hip[A-Za-z0-9_]+)", out))
+    assert imported, out
+    allocating = {n for n in imported if re.search(r"Malloc|Free|Alloc|HostRegister|MemPool", n)}
+    assert not allocating, sorted(allocating)
