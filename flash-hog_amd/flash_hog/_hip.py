@@ -87,7 +87,28 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    return torch._C._cuda_getCurrentRawStream(device.index)
+
+
+class _on_device:
+    """Makes `device` current for the duration of a kernel call (the C ABI
+    enqueues on the stream it is given, but the launch runs on the current
+    device); a no-op when it already is."""
+
+    __slots__ = ("index", "prev")
+
+    def __init__(self, device: torch.device):
+        self.index = device.index
+
+    def __enter__(self):
+        self.prev = torch.cuda.current_device()
+        if self.prev != self.index:
+            torch.cuda.set_device(self.index)
+
+    def __exit__(self, *exc):
+        if self.prev != self.index:
+            torch.cuda.set_device(self.prev)
+        return False
 
 
 def _check_inputs(named, dtype=None):
@@ -95,15 +116,20 @@ def _check_inputs(named, dtype=None):
     for name, t in named:
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"{name} must be a torch.Tensor")
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise ValueError(f"{name} must be on a GPU device, got {t.device}")
         if first is None:
             first = t
-        if t.device != first.device:
+            dev = t.get_device()
+        elif t.get_device() != dev:
             raise ValueError(f"{name} is on {t.device}, expected {first.device}")
         if dtype is not None and t.dtype != dtype:
             raise ValueError(f"{name} has dtype {t.dtype}, expected {dtype}")
     return first
+
+
+def _contig(*xs):
+    return tuple(x if x.is_contiguous() else x.contiguous() for x in xs)
 
 
 def _dims(q: torch.Tensor, k: torch.Tensor):
@@ -140,10 +166,10 @@ def attention_fwd(q, k, v, causal, scale: float):
     _check_inputs([("q", q), ("k", k), ("v", v)], q.dtype)
     B, Tq, Tk, N, Nk, Hd = _dims(q, k)
     _expect("v", v, k.shape)
-    q, k, v = (x.contiguous() for x in (q, k, v))
+    q, k, v = _contig(q, k, v)
     o = torch.empty_like(q)
     lse = torch.empty((B, N, Tq), device=q.device, dtype=torch.float32)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         check(lib().fhog_attention_fwd(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse),
             B, Tq, Tk, N, Nk, Hd, DTYPE_CODES[q.dtype], causal_code(causal), float(scale)))
@@ -159,10 +185,10 @@ def attention_bwd(q, k, v, o, dout, lse, causal, scale: float):
     _expect("o", o, q.shape)
     _expect("dout", dout, q.shape)
     _expect("lse", lse, (B, N, Tq), torch.float32)
-    q, k, v, o, dout, lse = (x.contiguous() for x in (q, k, v, o, dout, lse))
+    q, k, v, o, dout, lse = _contig(q, k, v, o, dout, lse)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     delta = torch.empty((B, N, Tq), device=q.device, dtype=torch.float32)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         check(lib().fhog_attention_bwd(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(dout), _ptr(lse),
             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(delta),
@@ -183,11 +209,10 @@ def attention_bwdbwd(q, k, v, o, dout, ddq, ddk, ddv, lse, causal, scale: float,
     for name, t in (("ddk", ddk), ("ddv", ddv)):
         _expect(name, t, k.shape)
     _expect("lse", lse, (B, N, Tq), torch.float32)
-    q, k, v, o, dout, ddq, ddk, ddv, lse = (
-        x.contiguous() for x in (q, k, v, o, dout, ddq, ddk, ddv, lse))
+    q, k, v, o, dout, ddq, ddk, ddv, lse = _contig(q, k, v, o, dout, ddq, ddk, ddv, lse)
     dq2, dk2, dv2, ddo = (torch.empty_like(x) for x in (q, k, v, dout))
     stats = torch.empty((3, B, N, Tq), device=q.device, dtype=torch.float32)
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         check(lib().fhog_attention_bwdbwd(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(dout),
             _ptr(ddq), _ptr(ddk), _ptr(ddv), _ptr(lse),
@@ -214,8 +239,7 @@ def attention_bwdbwd_noalloc(q, k, v, o, dout, ddq, ddk, ddv, lse, causal, scale
     for name, t in (("ddk", ddk), ("ddv", ddv)):
         _expect(name, t, k.shape)
     _expect("lse", lse, (B, N, Tq), torch.float32)
-    q, k, v, o, dout, ddq, ddk, ddv, lse = (
-        x.contiguous() for x in (q, k, v, o, dout, ddq, ddk, ddv, lse))
+    q, k, v, o, dout, ddq, ddk, ddv, lse = _contig(q, k, v, o, dout, ddq, ddk, ddv, lse)
     if out is None:
         out = tuple(torch.empty_like(x) for x in (q, k, v, dout))
     for name, t, like in zip(("dq2", "dk2", "dv2", "ddo"), out, (q, k, v, dout)):
@@ -223,7 +247,7 @@ def attention_bwdbwd_noalloc(q, k, v, o, dout, ddq, ddk, ddv, lse, causal, scale
         if not t.is_contiguous() or t.device != q.device:
             raise ValueError(f"{name} must be contiguous on {q.device}")
     dq2, dk2, dv2, ddo = out
-    with torch.cuda.device(q.device):
+    with _on_device(q.device):
         check(lib().fhog_attention_bwdbwd_noalloc(
             _stream(q.device), _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(dout),
             _ptr(ddq), _ptr(ddk), _ptr(ddv), _ptr(lse),

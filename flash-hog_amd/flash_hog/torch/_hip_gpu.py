@@ -147,12 +147,27 @@ _BwdBwdKernel = _kernel_function("flash_hog_attention_bwdbwd", attention_bwdbwd_
 
 
 # ---------------------------------------------------------------- wrappers
+#
+# Eager calls with gradient recording off (which is how the rules call them:
+# inside an autograd Function's forward, or inside a once-differentiable
+# backward) on plain GPU tensors, with no torch.func transform or compiler
+# trace active, go straight to the C ABI: the Function and the operator would only
+# add host time there (about 20 us per call), and their outputs would be the
+# same tensors.
+
+def _direct(*tensors) -> bool:
+    return (not torch.is_grad_enabled() and not torch._C._are_functorch_transforms_active()
+            and not torch.compiler.is_compiling() and tensors[0].is_cuda
+            and all(type(t) is torch.Tensor for t in tensors))
+
 
 def flash_fwd(query, key, value, *, mask_type: MaskType, scale: float | None):
     """Returns (out, activation): out like query, activation = L (B, N, T) fp32."""
     if query.ndim == 3:
         out, lse = flash_fwd(*_batchify(query, key, value), mask_type=mask_type, scale=scale)
         return out[0], lse[0]
+    if _direct(query, key, value):
+        return _hip.attention_fwd(query, key, value, causal_code(mask_type), _default_scale(query, scale))
     return _FwdKernel.apply(query, key, value, causal_code(mask_type), _default_scale(query, scale))
 
 
@@ -161,6 +176,9 @@ def flash_bwd(query, key, value, out, dO, activation, *, mask_type: MaskType, sc
     if query.ndim == 3:
         res = flash_bwd(*_batchify(query, key, value, out, dO, activation), mask_type=mask_type, scale=scale)
         return tuple(r[0] for r in res)
+    if _direct(query, key, value, out, dO, activation):
+        return _hip.attention_bwd(query, key, value, out, dO, activation, causal_code(mask_type),
+                                  _default_scale(query, scale))[:3]
     return _BwdKernel.apply(query, key, value, out, dO, activation, causal_code(mask_type),
                             _default_scale(query, scale))
 
@@ -170,4 +188,7 @@ def flash_bwdbwd(Q, K, V, O, dO, ddQ, ddK, ddV, L, *, mask_type: MaskType, scale
     if Q.ndim == 3:
         res = flash_bwdbwd(*_batchify(Q, K, V, O, dO, ddQ, ddK, ddV, L), mask_type=mask_type, scale=scale)
         return tuple(r[0] for r in res)
+    if _direct(Q, K, V, O, dO, ddQ, ddK, ddV, L):
+        return _hip.attention_bwdbwd(Q, K, V, O, dO, ddQ, ddK, ddV, L, causal_code(mask_type),
+                                     _default_scale(Q, scale))
     return _BwdBwdKernel.apply(Q, K, V, O, dO, ddQ, ddK, ddV, L, causal_code(mask_type), _default_scale(Q, scale))
