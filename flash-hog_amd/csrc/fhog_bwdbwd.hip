@@ -690,7 +690,7 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stage
   const int nkb = (p.nk + 32 * kWaves - 1) / (32 * kWaves);
   if (stages & 1) {
     hipError_t e;
-    if constexpr (sizeof(T) == 2 && D == 64) {
+    if constexpr (sizeof(T) == 2) {
       e = launch_bwdbwd_stage1_fused<T, D, CAUSAL>(p, stream);
     } else {
       const int npairs = p.batch * p.heads;

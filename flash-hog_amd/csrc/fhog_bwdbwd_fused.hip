@@ -1,6 +1,6 @@
 // Stage 1 of the Flash-HOG double backward (passes 1-3) in one sweep over the
-// keys, for 2-byte types at D = 64 (fhog_bwdbwd.hip holds the two-sweep
-// stage 1 used for the other shapes, and stage 2). The math follows
+// keys, for 2-byte types at D = 64 and 128 (fhog_bwdbwd.hip holds the
+// two-sweep stage 1 used for fp32, and stage 2). The math follows
 // flash_hog/_jax_refs/jax_impl.py:273-336 and the pass split of
 // flash_hog/jax/_pallas_gpu_kernel.py:149-278; outputs and row statistics are
 // those of fhog_bwdbwd.hip's stage 1.
@@ -25,7 +25,10 @@
 // beside the score tiles in the 256 registers of a wave that shares its SIMD
 // with another, and two co-resident waves are what overlaps one wave's matrix
 // work with the other's vector work. So a wave owns 16 queries and uses the
-// 16x16x32 matrix instruction (v_mfma_f32_16x16x32_{bf16,f16}):
+// 16x16x32 matrix instruction (v_mfma_f32_16x16x32_{bf16,f16}). At D = 128 this
+// still fits two waves per SIMD when each tile's scores are formed and then
+// finished (no pipelining): 2.78 ms at B2 N8192 H16 against 3.90 ms for the
+// two-sweep stage 1 at one wave per SIMD. Layouts:
 //   A (16 x 32): lane holds A[m = l % 16][k = 8 (l / 16) + e],   e = 0..7
 //   B (32 x 16): lane holds B[k = 8 (l / 16) + e][n = l % 16]
 //   C (16 x 16): lane holds C[m = 4 (l / 16) + i][n = l % 16],   i = 0..3
@@ -65,7 +68,12 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   constexpr int DB = D / 16;       // 16-wide output column blocks
   constexpr int BQ = kQ * kWaves;  // queries per workgroup
   constexpr int BK = 32;           // keys per streamed tile
-  constexpr int NST = 4;  // tiles t (finishing), t + 1 (scores), two in flight
+  // D = 64: a software-pipelined loop (the scores of tile t + 1 beside the
+  // element-wise step of tile t) over a 4-stage ring (64 KiB); D = 128: the
+  // accumulators and operands take twice the registers, so each tile's
+  // scores are formed and finished in turn, over a 2-stage ring (64 KiB).
+  constexpr bool PIPE = D == 64;
+  constexpr int NST = PIPE ? 4 : 2;  // tiles t (finishing), t + 1 (scores), two in flight
   constexpr int kTile = G::kElems * (int)sizeof(T);
   constexpr int kStage = 4 * kTile;  // K, V, ddK, ddV
   __shared__ __attribute__((aligned(1024))) char s_kv[NST * kStage];
@@ -256,7 +264,15 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   };
 
   int t = 0;
-  if (nfull > 0) {
+  if (!PIPE) {
+    for (; t < nfull; ++t) {
+      advance(t);
+      if (hi + 1 < nkt) issue(++hi);
+      Scores A;
+      scores(slot(t), A);
+      finish(slot(t), A, 0, std::false_type{});
+    }
+  } else if (nfull > 0) {
     Scores A, B;
     advance(0);
     scores(slot(0), A);
@@ -347,11 +363,16 @@ hipError_t launch_bwdbwd_stage1_fused(const BwdBwdParams<T>& p, hipStream_t stre
   return hipGetLastError();
 }
 
-#define FHOG_INST(T, C) template hipError_t launch_bwdbwd_stage1_fused<T, 64, C>(const BwdBwdParams<T>&, hipStream_t);
-FHOG_INST(__bf16, true)
-FHOG_INST(__bf16, false)
-FHOG_INST(_Float16, true)
-FHOG_INST(_Float16, false)
+#define FHOG_INST(T, D, C) \
+  template hipError_t launch_bwdbwd_stage1_fused<T, D, C>(const BwdBwdParams<T>&, hipStream_t);
+FHOG_INST(__bf16, 64, true)
+FHOG_INST(__bf16, 64, false)
+FHOG_INST(_Float16, 64, true)
+FHOG_INST(_Float16, 64, false)
+FHOG_INST(__bf16, 128, true)
+FHOG_INST(__bf16, 128, false)
+FHOG_INST(_Float16, 128, true)
+FHOG_INST(_Float16, 128, false)
 #undef FHOG_INST
 
 }  // namespace fhog
