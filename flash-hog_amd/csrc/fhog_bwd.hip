@@ -111,7 +111,7 @@ bwd_q_kernel(BwdParams<T> p, int chunk) {
   const uint32_t lds_tensor = lds_kv + tensor * kTile;
   auto issue = [&](int kt) {
     const int nvalid = p.nk - kt * BK;
-    const uint32_t dst = lds_tensor + (uint32_t)((kt % NST) * kStage);
+    const uint32_t dst = lds_tensor + (uint32_t)(((uint32_t)kt % NST) * kStage);
     const T* gsrc = src + (long)kt * BK * rsk;
     if (nvalid >= BK) {
       dma.issue(dst, gsrc);
@@ -133,7 +133,7 @@ bwd_q_kernel(BwdParams<T> p, int chunk) {
     __syncthreads();
     if (kt + NST - 1 < nkt) issue(kt + NST - 1);
     if (kt < wkt) {
-      const uint32_t sa = lds_kv + (uint32_t)((kt % NST) * kStage);  // K at 0, V at kTile
+      const uint32_t sa = lds_kv + (uint32_t)(((uint32_t)kt % NST) * kStage);  // K at 0, V at kTile
       f32x16 S = zero16(), dP = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -254,7 +254,7 @@ bwd_k_kernel(BwdParams<T> p, int chunk) {
     const uint32_t lds0 = lds_base_u32(s_q);
     auto issue = [&](int i, GroupCursor c) {
       const int q0t = (qt_begin + c.qt) * BQ;
-      const uint32_t stage = lds0 + (uint32_t)((i % NST) * kStage);
+      const uint32_t stage = lds0 + (uint32_t)(((uint32_t)i % NST) * kStage);
       const int nvalid = p.nq - q0t;
       const T* gsrc = src + (long)c.gi * D + (long)q0t * rs;
       const long sb = sbase + (long)c.gi * p.nq;
@@ -274,7 +274,7 @@ bwd_k_kernel(BwdParams<T> p, int chunk) {
     };
     auto finish_stats = [&](int i) {
       if (wave == kStatWave && g == 0) {
-        float* st = reinterpret_cast<float*>(s_q + (i % NST) * kStage + 2 * kTile);
+        float* st = reinterpret_cast<float*>(s_q + ((uint32_t)i % NST) * kStage + 2 * kTile);
         st[n] = -st[n] * inv_scale;
         st[kSR + n] = -st[kSR + n];
       }
@@ -309,8 +309,8 @@ bwd_k_kernel(BwdParams<T> p, int chunk) {
       const int q0 = (qt_begin + cur.qt) * BQ;
       const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
       if (active) {
-        const char* st = s_q + (i % NST) * kStage;
-        const uint32_t sa = lds0 + (uint32_t)((i % NST) * kStage);  // Q at 0, dO at kTile
+        const char* st = s_q + ((uint32_t)i % NST) * kStage;
+        const uint32_t sa = lds0 + (uint32_t)(((uint32_t)i % NST) * kStage);  // Q at 0, dO at kTile
         const float* sc = reinterpret_cast<const float*>(st + 2 * kTile);
         // S' = S_raw - L / scale, u = dP - D (register r holds query
         // 8 (r / 4) + 4 g + r % 4 of the tile)

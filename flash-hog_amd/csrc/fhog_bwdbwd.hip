@@ -159,7 +159,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p, int chunk) {
   auto issue = [&](int it) {
     const int kt = it < nkt ? it : it - nkt;
     const int nvalid = p.nk - kt * BK;
-    const uint32_t dst = lds_wave + (uint32_t)((it % NST) * kStage);
+    const uint32_t dst = lds_wave + (uint32_t)(((uint32_t)it % NST) * kStage);
     const T* gsrc = src + (long)kt * BK * rsk;
     if (nvalid >= BK) {
       dma.issue(dst, gsrc);
@@ -201,7 +201,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p, int chunk) {
     advance(it);
     if (it < wkt) {
       // stage tiles at sa + 0 (K), kTile (V), 2 kTile (ddK), 3 kTile (ddV)
-      const uint32_t sa = lds_kv + (uint32_t)((it % NST) * kStage);
+      const uint32_t sa = lds_kv + (uint32_t)(((uint32_t)it % NST) * kStage);
       f32x16 S = zero16(), ddS = zero16(), dP = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -263,7 +263,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p, int chunk) {
     const int kt = it - nkt;
     if (kt < wkt) {
       // stage tiles at sa + 0 (K), kTile (V), 2 kTile (ddK), 3 kTile (ddV)
-      const uint32_t sa = lds_kv + (uint32_t)((it % NST) * kStage);
+      const uint32_t sa = lds_kv + (uint32_t)(((uint32_t)it % NST) * kStage);
       f32x16 S = zero16(), ddS = zero16(), dP = zero16(), dPa = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
@@ -372,304 +372,267 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
   // B4 N2048 H16 D64 went from 149.7 to 144.8 us).
   const GridSlot slot = grid_slot(blockIdx.x, nbh, pairs ? (nkb + 1) / 2 : nkb, chunk);
   const int bh = slot.pair;
-  int kbs[2] = {slot.rank, nkb - 1 - slot.rank};
-  if (pairs == 2) kbs[1] += slot.rank < nkb / 4 ? -(nkb / 4) : nkb / 4;
-  const int nblk = (pairs && kbs[1] != kbs[0]) ? 2 : 1;
-
-  const int b = bh / p.kv_heads, hk = bh % p.kv_heads;
-  const int grp = p.heads / p.kv_heads;  // query heads per key/value head
-  const long rs = (long)p.heads * D;      // query-side row stride
-  const long rsk = (long)p.kv_heads * D;  // key-side row stride
-  // query head hk * grp + gi: tensors at qbase + gi * D, statistics at sbase + gi * nq
-  const long qbase = ((long)b * p.nq * p.heads + (long)hk * grp) * D;
-  const long kbase = ((long)b * p.nk * p.kv_heads + hk) * D;
-  const long sbase = ((long)b * p.heads + (long)hk * grp) * p.nq;
-  const float scale = p.scale;
-
-  // Block bi visits query tiles qt_begin(bi) .. nqt - 1, each for every head
-  // of the group: iteration i is query tile qt_begin + i / grp of query head
-  // hk * grp + i % grp (the group reduction of
-  // flash_hog/jax/_pallas_gpu_kernel.py:333-370, in one ring). One ring runs
-  // through the iterations of both blocks, so the first tiles of the second
-  // block stream in during the last iterations of the first and the
-  // workgroup never waits for a refill (the block change cost 7.3 us per
-  // workgroup with a ring per block, 2.8 us more than the kernel's own start).
-  const int nqt = (p.nq + BQ - 1) / BQ;
-  auto qt_begin_of = [&](int bi) { return CAUSAL ? max(0, kbs[bi] * BKB - p.coff) / BQ : 0; };
-  int tot[2];
-#pragma unroll
-  for (int bi = 0; bi < 2; ++bi) tot[bi] = bi < nblk ? max(0, nqt - qt_begin_of(bi)) * grp : 0;
-  // (uniform; saying so keeps the compiler from treating the loops as divergent)
-  const int gtotal = __builtin_amdgcn_readfirstlane(tot[0] + tot[1]);
-
-  SwzFrags<T, D> fr;
-  fr.init(lane);
-  const T* src = (wave == 0 ? p.q : wave == 1 ? p.dout : p.ddq) + qbase;
-  const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
-  TileDma<T, D> dma;
-  dma.init(row_bytes, BQ, lane);
-  const uint32_t lds_q = lds_base_u32(s_q);
-  const uint32_t lds_wave = lds_q + wave * kTile;
-  // Next head of the group: D elements on; next query tile of the first head:
-  // BQ rows on from the first head.
-  const long row_step = (long)BQ * rs - (long)(grp - 1) * D;
-
-  // Issue cursor: the next tile to stream is iteration `nxt` of block `ib`
-  // (ileft of its iterations not yet issued), from gnext.
-  int ib = 0, ileft = tot[0], qtb_issue = qt_begin_of(0);
-  GroupCursor nxt;
-  const T* gnext = src + (long)qtb_issue * BQ * rs;
-  auto next_block = [&]() {
-    if (ileft == 0 && ib + 1 < nblk) {
-      ib = 1;
-      ileft = tot[1];
-      qtb_issue = qt_begin_of(1);
-      nxt = GroupCursor{};
-      gnext = src + (long)qtb_issue * BQ * rs;
-    }
-  };
-  next_block();  // an empty first block
-
-  // Wave 3 streams the per-query statistics of each tile with two dword DMAs
-  // (lanes 0-31 then 32-63: L and D, then dD and B; rows past nq repeat row
-  // nq - 1) into the tile's stage, and once they have landed rewrites them in
-  // place as the initial values of the four score accumulators:
-  // -L / scale, -dD / scale, -D, -(D dD + B) (-L and -dD when K and ddK carry
-  // the scale).
-  constexpr int kStatLoads = 4;  // two per lane half
-  const float inv_scale = 1.0f / scale;
-  auto finish_stats = [&](int gi) {
-    if (g == 0) {
-      float* st = reinterpret_cast<float*>(s_q + (gi % NST) * kStage + 3 * kTile);
-      const float L = st[n], Dq = st[BQ + n], dDq = st[2 * BQ + n], Bq = st[3 * BQ + n];
-      st[n] = PRE ? -L : -L * inv_scale;
-      st[BQ + n] = PRE ? -dDq : -dDq * inv_scale;
-      st[2 * BQ + n] = -Dq;
-      st[3 * BQ + n] = -fmaf(Dq, dDq, Bq);
-    }
-  };
-  // Waits (wave 3) until the statistics of iteration gi have landed: the DMAs
-  // of later iterations, at most NST - 2 of them, may still be in flight.
-  auto wait_stats = [&](int gi) {
-    if constexpr (NST >= 3) {
-      if (gi + NST - 2 < gtotal) {
-        wait_vmem_le<(NST - 2) * kStatLoads>();
-        return;
-      }
-    }
-    wait_vmem_le<0>();
-  };
-  // Streams global iteration gi (the cursor's position) into its ring stage,
-  // then moves the cursor on.
-  auto issue_next = [&](int gi) {
-    const int qt = qtb_issue + nxt.qt;
-    if (wave == 3) {
-      // uniform row base plus a per-lane offset; each lane half loads its own tensor
-      const uint32_t off = 4u * (uint32_t)min(qt * BQ + n, p.nq - 1);
-      const long sb = sbase + (long)nxt.gi * p.nq;
-      const uint32_t dst = lds_q + (uint32_t)((gi % NST) * kStage + 3 * kTile);
-      if (g == 0) {
-        dma4s(p.lse + sb, off, dst);
-        dma4s(p.ddelta + sb, off, dst + 256);
-      } else {
-        dma4s(p.delta + sb, off, dst);
-        dma4s(p.bstat + sb, off, dst + 256);
-      }
-    } else {
-      const uint32_t dst = lds_wave + (uint32_t)((gi % NST) * kStage);
-      if (qt * BQ + BQ <= p.nq) {
-        dma.issue(dst, gnext);
-      } else {  // the ragged last query tile (offsets made here: registers are scarce)
-        TileDma<T, D> part;
-        part.init(row_bytes, p.nq - qt * BQ, lane);
-        part.issue(dst, gnext);
-      }
-    }
-    gnext += nxt.gi + 1 == grp ? row_step : (long)D;
-    nxt.next(grp);
-    --ileft;
-    next_block();
-  };
-
-  // Key-side operands (B of the score products) of key block kb, addressed as
-  // the block's first row (uniform) plus a 32-bit per-lane offset, so that no
-  // 64-bit per-lane address stays live from one block to the next.
-  V8<T> kf[KS], dkf[KS], vf[KS], dvf[KS];
-  auto load_keys = [&](int kb) {
-    const int r = wave * 32 + n;  // key row within the block
-    const long rowb = kbase + (long)kb * BKB * rsk;
-    uint32_t lo = (uint32_t)r * (uint32_t)rsk + 8u * (uint32_t)g;
-    // (opaque to the compiler, so that the addresses are formed here and not
-    // kept live across a whole block's loop)
-    asm volatile("" : "+v"(lo));
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const uint32_t off = lo + 16u * (uint32_t)ks;
-      if (kb * BKB + r < p.nk) {
-        kf[ks] = *reinterpret_cast<const V8<T>*>(p.k + rowb + off);
-        dkf[ks] = *reinterpret_cast<const V8<T>*>(p.ddk + rowb + off);
-        vf[ks] = *reinterpret_cast<const V8<T>*>(p.v + rowb + off);
-        dvf[ks] = *reinterpret_cast<const V8<T>*>(p.ddv + rowb + off);
-      } else {
-        kf[ks] = zero8<T>();
-        dkf[ks] = zero8<T>();
-        vf[ks] = zero8<T>();
-        dvf[ks] = zero8<T>();
-      }
-    }
-  };
-
-  // The ring's first tiles go out before the key-side loads, so that both
-  // latencies overlap (this also shortens the loads' live ranges).
-#pragma unroll
-  for (int i = 0; i < NST - 1; ++i)
-    if (i < gtotal) issue_next(i);
-  load_keys(kbs[0]);
-  const float c2 = PRE ? kLog2e : scale * kLog2e;
-
-  int gbase = 0;  // global iteration of the current block's first tile
-  for (int bi = 0; bi < nblk; ++bi) {
-    const int k0 = kbs[bi] * BKB + wave * 32;
+  const int first = slot.rank;
+  int second = nkb - 1 - slot.rank;
+  if (pairs == 2) second += slot.rank < nkb / 4 ? -(nkb / 4) : nkb / 4;
+  const int nblk = (pairs && second != first) ? 2 : 1;
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int kb = blk == 0 ? first : second;
+    if (blk > 0) __syncthreads();  // every wave is done with the previous block's ring
+    const int b = bh / p.kv_heads, hk = bh % p.kv_heads;
+    const int grp = p.heads / p.kv_heads;  // query heads per key/value head
+    const long rs = (long)p.heads * D;      // query-side row stride
+    const long rsk = (long)p.kv_heads * D;  // key-side row stride
+    // query head hk * grp + gi: tensors at qbase + gi * D, statistics at sbase + gi * nq
+    const long qbase = ((long)b * p.nq * p.heads + (long)hk * grp) * D;
+    const long kbase = ((long)b * p.nk * p.kv_heads + hk) * D;
+    const long sbase = ((long)b * p.heads + (long)hk * grp) * p.nq;
+    const int k0 = kb * BKB + wave * 32;
     const int kj = k0 + n;
-    const int qt_begin = qt_begin_of(bi);
-    const int total = __builtin_amdgcn_readfirstlane(tot[bi]);
+    const bool kvalid = kj < p.nk;
 
-    // Retire the key-side loads (and with them the ring's tiles issued so far,
-    // and the previous block's stores) before the loop: vmcnt counts the
-    // untracked LDS DMAs too, so a wait for the loads inside the loop would
-    // drain the prefetched tiles.
-    wait_vmem();
-    if constexpr (PRE) {
-      // scale is a power of two: K and ddK carry it exactly, so S and ddS come
-      // out of the matrix products already scaled (bit-identical to scaling
-      // them afterwards) and the element-wise step skips one multiply.
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          kf[ks][e] = (T)((float)kf[ks][e] * scale);
-          dkf[ks][e] = (T)((float)dkf[ks][e] * scale);
-        }
-    }
-    if (wave == 3 && bi == 0 && gtotal > 0) {
-      wait_stats(0);
-      finish_stats(0);
-    }
+    // Iteration i visits query tile qt_begin + i / grp of query head
+    // hk * grp + i % grp (the group reduction of
+    // flash_hog/jax/_pallas_gpu_kernel.py:333-370, in one ring).
+    const int nqt = (p.nq + BQ - 1) / BQ;
+    const int qt_begin = CAUSAL ? max(0, kb * BKB - p.coff) / BQ : 0;
 
     f32x16 acc_dk2[DT], acc_dv2[DT];
-#pragma unroll
+  #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       acc_dk2[dt] = zero16();
       acc_dv2[dt] = zero16();
     }
 
-    GroupCursor cur;  // iteration i of this block
-    for (int i = 0; i < total; ++i, cur.next(grp)) {
-      const int gi = gbase + i;
-      if (wave < 3) wait_tile<NST, G::kLoads>(gi, gtotal);
-      __syncthreads();
-      if (gi + NST - 1 < gtotal) issue_next(gi + NST - 1);
-      const int q0 = (qt_begin + cur.qt) * BQ;
-      const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
-      if (active) {
-        const char* st = s_q + (gi % NST) * kStage;
-        const uint32_t sa = lds_q + (uint32_t)((gi % NST) * kStage);  // tiles: Q, dO, ddQ
-        const float* sc = reinterpret_cast<const float*>(st + 3 * kTile);
-        // The accumulators start at the per-query constants (register r holds
-        // query 8 (r / 4) + 4 g + r % 4 of the tile), so they end as
-        //   S' = S_raw - L / scale, ddS' = ddS_raw - dD / scale,
-        //   u = dP - D, dPa' = dPa - (D dD + B).
-        f32x16 S, ddS, dP, dPa;
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          const int m0 = 8 * a + 4 * g;
-          const f32x4 c0 = *reinterpret_cast<const f32x4*>(sc + m0);
-          const f32x4 c1 = *reinterpret_cast<const f32x4*>(sc + BQ + m0);
-          const f32x4 c2v = *reinterpret_cast<const f32x4*>(sc + 2 * BQ + m0);
-          const f32x4 c3 = *reinterpret_cast<const f32x4*>(sc + 3 * BQ + m0);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            S[4 * a + j] = c0[j];
-            ddS[4 * a + j] = c1[j];
-            dP[4 * a + j] = c2v[j];
-            dPa[4 * a + j] = c3[j];
+    if (qt_begin < nqt) {
+      const float scale = p.scale;
+      SwzFrags<T, D> fr;
+      fr.init(lane);
+
+      const int total = (nqt - qt_begin) * grp;
+      const T* src = (wave == 0 ? p.q : wave == 1 ? p.dout : p.ddq) + qbase;
+      const uint32_t row_bytes = (uint32_t)(rs * (long)sizeof(T));
+      TileDma<T, D> dma;
+      dma.init(row_bytes, BQ, lane);
+      const uint32_t lds_q = lds_base_u32(s_q);
+      const uint32_t lds_wave = lds_q + wave * kTile;
+      // Source of the next tile to issue, advanced with the cursor: the next head
+      // of the group is D elements on, the next query tile of the first head
+      // BQ rows on from the first head.
+      const T* gnext = src + (long)qt_begin * BQ * rs;
+      const long row_step = (long)BQ * rs - (long)(grp - 1) * D;
+
+      // Wave 3 streams the per-query statistics of each tile with two dword DMAs
+      // (lanes 0-31 then 32-63: L and D, then dD and B; rows past nq repeat row
+      // nq - 1) into the tile's stage, and once they have landed rewrites them in
+      // place as the initial values of the four score accumulators:
+      // -L / scale, -dD / scale, -D, -(D dD + B) (-L and -dD when K and ddK carry
+      // the scale).
+      constexpr int kStatLoads = 4;  // two per lane half
+      auto issue_stats = [&](int i, GroupCursor c) {
+        // uniform row base plus a per-lane offset; each lane half loads its own tensor
+        const uint32_t off = 4u * (uint32_t)min((qt_begin + c.qt) * BQ + n, p.nq - 1);
+        const long sb = sbase + (long)c.gi * p.nq;
+        const uint32_t dst = lds_base_u32(s_q) + (uint32_t)((i % NST) * kStage + 3 * kTile);
+        if (g == 0) {
+          dma4s(p.lse + sb, off, dst);
+          dma4s(p.ddelta + sb, off, dst + 256);
+        } else {
+          dma4s(p.delta + sb, off, dst);
+          dma4s(p.bstat + sb, off, dst + 256);
+        }
+      };
+      const float inv_scale = 1.0f / scale;
+      auto finish_stats = [&](int i) {
+        if (g == 0) {
+          float* st = reinterpret_cast<float*>(s_q + (i % NST) * kStage + 3 * kTile);
+          const float L = st[n], Dq = st[BQ + n], dDq = st[2 * BQ + n], Bq = st[3 * BQ + n];
+          st[n] = PRE ? -L : -L * inv_scale;
+          st[BQ + n] = PRE ? -dDq : -dDq * inv_scale;
+          st[2 * BQ + n] = -Dq;
+          st[3 * BQ + n] = -fmaf(Dq, dDq, Bq);
+        }
+      };
+      // Waits (wave 3) until the statistics of tile i have landed: the DMAs of
+      // later tiles, at most NST - 2 of them, may still be in flight.
+      auto wait_stats = [&](int i) {
+        if constexpr (NST >= 3) {
+          if (i + NST - 2 < total) {
+            wait_vmem_le<(NST - 2) * kStatLoads>();
+            return;
           }
         }
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const V8<T> qa = fr.rowf(sa, 0, ks);
-          const V8<T> dqa = fr.rowf(sa, 2 * kTile, ks);
-          const V8<T> doa = fr.rowf(sa, kTile, ks);
-          S = mma<T>(qa, kf[ks], S);
-          ddS = mma<T>(dqa, kf[ks], ddS);
-          ddS = mma<T>(qa, dkf[ks], ddS);
-          dP = mma<T>(doa, vf[ks], dP);
-          dPa = mma<T>(doa, dvf[ks], dPa);
+        wait_vmem_le<0>();
+      };
+      auto issue = [&](int i, GroupCursor c) {
+        if (wave == 3) {
+          issue_stats(i, c);
+          return;
         }
-        f32x16 P;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) P[r] = exp2_fast(S[r] * c2);
-        const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31 - p.coff);
-        if (need_mask) {
-          // visible iff query >= key - coff (causal) and query < nq
-          const int qlo = (CAUSAL ? kj - p.coff : 0) - q0, qhi = p.nq - q0;
-          // (the row indices are formed here, on the few masked tiles, rather
-          // than held in 16 registers for the whole loop)
-          int gm = g;
-          asm volatile("" : "+v"(gm));
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int m = crow(r, gm);
-            if (m < qlo || m >= qhi) P[r] = 0.f;
-          }
+        const int q0t = (qt_begin + c.qt) * BQ;
+        const uint32_t dst = lds_wave + (uint32_t)((i % NST) * kStage);
+        if (q0t + BQ <= p.nq) {
+          dma.issue(dst, gnext);
+        } else {  // the ragged last query tile (offsets made here: registers are scarce)
+          TileDma<T, D> part;
+          part.init(row_bytes, p.nq - q0t, lane);
+          part.issue(dst, gnext);
         }
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          f32x8 vdS, vdS2, vddP;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int r = 8 * s + e;
-            const float t = PRE ? ddS[r] : ddS[r] * scale;  // ddS - dD
-            const float x = fmaf(dP[r], t, dPa[r]);      // dP2 - B
-            vdS[e] = P[r] * dP[r];
-            vdS2[e] = P[r] * x;
-            vddP[e] = P[r] * t;
-          }
-          const V8<T> oS = cvt8<T>(vdS);
-          const V8<T> oS2 = cvt8<T>(vdS2);
-          const V8<T> odP = cvt8<T>(vddP);
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            acc_dk2[dt] = mma<T>(fr.trf(sa, 2 * kTile, dt, s), oS, acc_dk2[dt]);
-            acc_dk2[dt] = mma<T>(fr.trf(sa, 0, dt, s), oS2, acc_dk2[dt]);
-            acc_dv2[dt] = mma<T>(fr.trf(sa, kTile, dt, s), odP, acc_dv2[dt]);
-          }
+      };
+      auto advance = [&](GroupCursor& c) {
+        gnext += c.gi + 1 == grp ? row_step : (long)D;
+        c.next(grp);
+      };
+      // The ring's first tiles go out before the key-side loads, so that both
+      // latencies overlap (this also shortens the loads' live ranges).
+      GroupCursor nxt;  // iteration of the next tile to issue
+  #pragma unroll
+      for (int i = 0; i < NST - 1; ++i)
+        if (i < total) {
+          issue(i, nxt);
+          advance(nxt);
+        }
+
+      // Key-side operands (B of the score products).
+      V8<T> kf[KS], dkf[KS], vf[KS], dvf[KS];
+  #pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const long off = kbase + (long)kj * rsk + 16 * ks + 8 * g;
+        if (kvalid) {
+          kf[ks] = *reinterpret_cast<const V8<T>*>(p.k + off);
+          dkf[ks] = *reinterpret_cast<const V8<T>*>(p.ddk + off);
+          vf[ks] = *reinterpret_cast<const V8<T>*>(p.v + off);
+          dvf[ks] = *reinterpret_cast<const V8<T>*>(p.ddv + off);
+        } else {
+          kf[ks] = zero8<T>();
+          dkf[ks] = zero8<T>();
+          vf[ks] = zero8<T>();
+          dvf[ks] = zero8<T>();
         }
       }
-      // Iteration gi + 1's statistics (possibly the next block's first) are
-      // read after the next barrier.
-      if (wave == 3 && gi + 1 < gtotal) {
-        wait_stats(gi + 1);
-        finish_stats(gi + 1);
+      if constexpr (PRE) {
+        // scale is a power of two: K and ddK carry it exactly, so S and ddS come
+        // out of the matrix products already scaled (bit-identical to scaling
+        // them afterwards) and the element-wise step skips one multiply.
+  #pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            kf[ks][e] = (T)((float)kf[ks][e] * scale);
+            dkf[ks][e] = (T)((float)dkf[ks][e] * scale);
+          }
+      }
+      const float c2 = PRE ? kLog2e : scale * kLog2e;
+
+      // Retire the key-side loads (and with them the first tiles) before the
+      // loop: vmcnt counts the untracked LDS DMAs too, so a wait for the loads
+      // inside the loop would drain the prefetched tiles.
+      wait_vmem();
+      if (wave == 3) {
+        wait_stats(0);
+        finish_stats(0);
+      }
+
+      GroupCursor cur;  // iteration i
+      for (int i = 0; i < total; ++i, cur.next(grp)) {
+        if (wave < 3) wait_tile<NST, G::kLoads>(i, total);
+        __syncthreads();
+        if (i + NST - 1 < total) {
+          issue(i + NST - 1, nxt);
+          advance(nxt);
+        }
+        const int q0 = (qt_begin + cur.qt) * BQ;
+        const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
+        if (active) {
+          const char* st = s_q + (i % NST) * kStage;
+          const uint32_t sa = lds_q + (uint32_t)((i % NST) * kStage);  // tiles: Q, dO, ddQ
+          const float* sc = reinterpret_cast<const float*>(st + 3 * kTile);
+          // The accumulators start at the per-query constants (register r holds
+          // query 8 (r / 4) + 4 g + r % 4 of the tile), so they end as
+          //   S' = S_raw - L / scale, ddS' = ddS_raw - dD / scale,
+          //   u = dP - D, dPa' = dPa - (D dD + B).
+          f32x16 S, ddS, dP, dPa;
+  #pragma unroll
+          for (int a = 0; a < 4; ++a) {
+            const int m0 = 8 * a + 4 * g;
+            const f32x4 c0 = *reinterpret_cast<const f32x4*>(sc + m0);
+            const f32x4 c1 = *reinterpret_cast<const f32x4*>(sc + BQ + m0);
+            const f32x4 c2v = *reinterpret_cast<const f32x4*>(sc + 2 * BQ + m0);
+            const f32x4 c3 = *reinterpret_cast<const f32x4*>(sc + 3 * BQ + m0);
+  #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              S[4 * a + j] = c0[j];
+              ddS[4 * a + j] = c1[j];
+              dP[4 * a + j] = c2v[j];
+              dPa[4 * a + j] = c3[j];
+            }
+          }
+  #pragma unroll
+          for (int ks = 0; ks < KS; ++ks) {
+            const V8<T> qa = fr.rowf(sa, 0, ks);
+            const V8<T> dqa = fr.rowf(sa, 2 * kTile, ks);
+            const V8<T> doa = fr.rowf(sa, kTile, ks);
+            S = mma<T>(qa, kf[ks], S);
+            ddS = mma<T>(dqa, kf[ks], ddS);
+            ddS = mma<T>(qa, dkf[ks], ddS);
+            dP = mma<T>(doa, vf[ks], dP);
+            dPa = mma<T>(doa, dvf[ks], dPa);
+          }
+          f32x16 P;
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) P[r] = exp2_fast(S[r] * c2);
+          const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31 - p.coff);
+          if (need_mask) {
+            // visible iff query >= key - coff (causal) and query < nq
+            const int qlo = (CAUSAL ? kj - p.coff : 0) - q0, qhi = p.nq - q0;
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int m = crow(r, g);
+              if (m < qlo || m >= qhi) P[r] = 0.f;
+            }
+          }
+  #pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            f32x8 vdS, vdS2, vddP;
+  #pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int r = 8 * s + e;
+              const float t = PRE ? ddS[r] : ddS[r] * scale;  // ddS - dD
+              const float x = fmaf(dP[r], t, dPa[r]);      // dP2 - B
+              vdS[e] = P[r] * dP[r];
+              vdS2[e] = P[r] * x;
+              vddP[e] = P[r] * t;
+            }
+            const V8<T> oS = cvt8<T>(vdS);
+            const V8<T> oS2 = cvt8<T>(vdS2);
+            const V8<T> odP = cvt8<T>(vddP);
+  #pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+              acc_dk2[dt] = mma<T>(fr.trf(sa, 2 * kTile, dt, s), oS, acc_dk2[dt]);
+              acc_dk2[dt] = mma<T>(fr.trf(sa, 0, dt, s), oS2, acc_dk2[dt]);
+              acc_dv2[dt] = mma<T>(fr.trf(sa, kTile, dt, s), odP, acc_dv2[dt]);
+            }
+          }
+        }
+        // Tile i + 1's statistics are read after the next barrier.
+        if (wave == 3 && i + 1 < total) {
+          wait_stats(i + 1);
+          finish_stats(i + 1);
+        }
       }
     }
-    gbase += total;
 
-    // The next block's key-side loads go out before this block's stores, so
-    // that their latencies overlap.
-    if (bi + 1 < nblk) load_keys(kbs[bi + 1]);
-    if (kj < p.nk) {
-      uint32_t orow = (uint32_t)(wave * 32 + n) * (uint32_t)rsk;
-      asm volatile("" : "+v"(orow));  // (formed here, see load_keys)
-      T* dk2 = p.dk2 + kbase + (long)kbs[bi] * BKB * rsk + orow;
-      T* dv2 = p.dv2 + kbase + (long)kbs[bi] * BKB * rsk + orow;
-#pragma unroll
+    if (kvalid) {
+      const float scale = p.scale;
+      T* dk2 = p.dk2 + kbase + (long)kj * rsk;
+      T* dv2 = p.dv2 + kbase + (long)kj * rsk;
+  #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
+  #pragma unroll
         for (int a = 0; a < 4; ++a) {
           const int d = 32 * dt + 8 * a + 4 * g;
           f32x4 x, y;
-#pragma unroll
+  #pragma unroll
           for (int j = 0; j < 4; ++j) {
             x[j] = acc_dk2[dt][4 * a + j] * scale;
             y[j] = acc_dv2[dt][4 * a + j];

@@ -161,7 +161,7 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   wait_vmem();
   auto issue = [&](int kt) {
     const int nvalid = p.nk - kt * BK;
-    const uint32_t dst = lds_wave + (uint32_t)((kt % NST) * kStage);
+    const uint32_t dst = lds_wave + (uint32_t)(((uint32_t)kt % NST) * kStage);
     const T* gsrc = gnext;
     gnext += BK * rsk;
     if (nvalid >= BK) {
@@ -233,7 +233,7 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
       acc_o[db] = mma16<T>(fr.trf(sa, kTile, db), ox, acc_o[db]);
     }
   };
-  auto slot = [&](int kt) { return lds_kv + (uint32_t)((kt % NST) * kStage); };
+  auto slot = [&](int kt) { return lds_kv + (uint32_t)(((uint32_t)kt % NST) * kStage); };
   // Waits for tile `need` and makes every wave's copy visible; `hi` is the last
   // tile issued (tiles after `need`, at most NST - 2, may still be in flight).
   auto advance = [&](int need) {

@@ -96,7 +96,7 @@ fwd_kernel(FwdParams<T> p, int chunk) {
   const uint32_t lds_tensor = lds_kv + tensor * kTile;
   auto issue = [&](int kt) {
     const int nvalid = p.nk - kt * BK;
-    const uint32_t dst = lds_tensor + (uint32_t)((kt % NST) * kStage);
+    const uint32_t dst = lds_tensor + (uint32_t)(((uint32_t)kt % NST) * kStage);
     const T* gsrc = src + (long)kt * BK * rsk;
     if (nvalid >= BK) {
       dma.issue(dst, gsrc);
@@ -128,7 +128,7 @@ fwd_kernel(FwdParams<T> p, int chunk) {
     __syncthreads();
     if (kt + NST - 1 < nkt) issue(kt + NST - 1);
     if (kt < wkt) {
-      const uint32_t sa = lds_kv + (uint32_t)((kt % NST) * kStage);  // K at 0, V at kTile
+      const uint32_t sa = lds_kv + (uint32_t)(((uint32_t)kt % NST) * kStage);  // K at 0, V at kTile
       f32x16 S = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) S = mma<T>(fr.rowf(sa, 0, ks), qf[ks], S);
