@@ -178,9 +178,14 @@ def hvp_table(args):
     iterations, 5 at sequence >= 16k, 3 at >= 64k) and faithfulness: cosine
     similarity and max relative error of the concatenated (q, k, v) HVP against
     a dense fp32 torch-autograd HVP of the same function where that fits
-    (batch * sequence^2 <= 2048^2), else against the same HVP through this
-    library's fp32 kernels (sequence <= 16384), else not measured."""
+    (batch * sequence^2 <= 2048^2), else, on two (batch, head) slices (the
+    first and the last), against the fp32 closed form of the attention double
+    backward evaluated a block of query rows at a time
+    (tests/gpu_reference.py, pinned to the fp64 oracle by the GPU tests)."""
     import torch
+
+    sys.path.insert(0, str(REPO / "tests"))
+    import gpu_reference
 
     import flash_hog
 
@@ -237,6 +242,22 @@ def hvp_table(args):
         del graph, out
         return e0.elapsed_time(e1) / iters
 
+    def hvp_slices(x, cot, tan, slices):
+        """The HVP on (batch, head) slices: (q, k, v) cotangents of the double
+        backward with residual (x, O, L, dO = cot) and cotangents tan, with O, L
+        from the fp32 forward of x; attention heads are independent, so a slice
+        of the full HVP is the HVP of that slice."""
+        out = []
+        for b, h in slices:
+            sl = lambda t: t[b, :, h, :].contiguous()
+            q, k, v = (sl(t) for t in x)
+            rows = max(128, min(4096, (1 << 28) // q.shape[0]))
+            o, lse = gpu_reference.fwd_head_chunked(q, k, v, scale, True, rows=rows)
+            dq2, dk2, dv2, _ = gpu_reference.bwdbwd_head_chunked(
+                q, k, v, o, sl(cot), *(sl(t) for t in tan), lse, scale, True, rows=rows)
+            out += [dq2, dk2, dv2]
+        return out
+
     def compare(a, r):
         a = torch.cat([t.double().flatten() for t in a])
         r = torch.cat([t.double().flatten() for t in r])
@@ -269,10 +290,10 @@ def hvp_table(args):
         gms = graph_ms(f, x, cot, tan, iters) if N <= GRAPH_MAX_SEQ else None
         if B * N * N <= 2048 * 2048:
             ref, against = hvp(attn_dense, x, cot, tan), "dense fp32"
-        elif N <= 16384:
-            ref, against = hvp(attn_flash(torch.float32), x, cot, tan), "fp32 kernels"
         else:
-            ref, against = None, None
+            slices = [(0, 0), (B - 1, H - 1)]
+            ref, against = hvp_slices(x, cot, tan, slices), "fp32 closed form, 2 heads"
+            out = [t[b, :, h, :] for b, h in slices for t in out]
         faith = "not measured"
         row = {"table": args.hvp_table, "batch": B, "seq": N, "heads": H, "head_dim": D, "hvp_ms": round(ms, 4),
                "hvp_graph_ms": None if gms is None else round(gms, 4), "iterations": iters}

@@ -6,6 +6,7 @@
 #include <stdint.h>
 #include <stdio.h>
 #include <stdarg.h>
+#include <string.h>
 
 #include <atomic>
 #include <mutex>
@@ -108,7 +109,7 @@ hipError_t dispatch(int dtype, int head_dim, bool causal, F&& f) {
 
 extern "C" {
 
-int fhog_abi_version(void) { return 102; }
+int fhog_abi_version(void) { return 103; }
 
 const char* fhog_status_string(int status) {
   switch (status) {
@@ -121,6 +122,23 @@ const char* fhog_status_string(int status) {
 }
 
 const char* fhog_last_error(void) { return g_last_error; }
+
+int fhog_attention_supported(int device, int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim,
+                             int dtype, int causal, float scale) {
+  static const char* who = "fhog_attention_supported";
+  const Shape s{batch, n_q, n_k, heads, kv_heads, head_dim, dtype, causal, scale};
+  if (int st = check_shape(s, who)) return st;
+  if (device >= 0) {
+    hipDeviceProp_t prop;
+    const hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess)
+      return fail(FHOG_ERR_UNSUPPORTED, "%s: no HIP device %d (%s)", who, device, hipGetErrorString(e));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+      return fail(FHOG_ERR_UNSUPPORTED, "%s: device %d is %s; the kernels are built for gfx950", who, device,
+                  prop.gcnArchName);
+  }
+  return ok();
+}
 
 size_t fhog_row_stat_bytes(int batch, int heads, int n_q) {
   if (batch < 1 || heads < 1 || n_q < 1) return 0;

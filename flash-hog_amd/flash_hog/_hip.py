@@ -40,6 +40,7 @@ SIGNATURES = {
     "fhog_status_string": (ctypes.c_char_p, [_i]),
     "fhog_last_error": (ctypes.c_char_p, []),
     "fhog_row_stat_bytes": (ctypes.c_size_t, [_i, _i, _i]),
+    "fhog_attention_supported": (_i, [_i] * 9 + [_f]),
     "fhog_attention_fwd": (_i, [_p, _p, _p, _p, _p, _p] + [_i] * 8 + [_f]),
     "fhog_attention_bwd": (_i, [_p] * 11 + [_i] * 8 + [_f]),
     "fhog_attention_bwdbwd": (_i, [_p] * 17 + [_i] * 8 + [_f]),
@@ -159,6 +160,18 @@ def _expect(name, t, shape, dtype=None):
         raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
     if dtype is not None and t.dtype != dtype:
         raise ValueError(f"{name} has dtype {t.dtype}, expected {dtype}")
+
+
+def attention_supported(batch: int, n_q: int, n_k: int, heads: int, kv_heads: int, head_dim: int, dtype,
+                        causal, scale: float, device: int = -1) -> tuple[bool, str]:
+    """(True, "") if the library has kernels for these arguments (and, for
+    device >= 0, that HIP device is a gfx950 GPU), else (False, the reason the
+    entry points would give). Launches and allocates nothing."""
+    if dtype not in DTYPE_CODES:
+        return False, f"unsupported dtype {dtype}"
+    status = lib().fhog_attention_supported(int(device), batch, n_q, n_k, heads, kv_heads, head_dim,
+                                            DTYPE_CODES[dtype], causal_code(causal), float(scale))
+    return status == 0, "" if status == 0 else lib().fhog_last_error().decode()
 
 
 def attention_fwd(q, k, v, causal, scale: float):

@@ -192,3 +192,36 @@ def flash_bwdbwd(Q, K, V, O, dO, ddQ, ddK, ddV, L, *, mask_type: MaskType, scale
         return _hip.attention_bwdbwd(Q, K, V, O, dO, ddQ, ddK, ddV, L, causal_code(mask_type),
                                      _default_scale(Q, scale))
     return _BwdBwdKernel.apply(Q, K, V, O, dO, ddQ, ddK, ddV, L, causal_code(mask_type), _default_scale(Q, scale))
+
+
+# ------------------------------------------------------------- capability
+
+def supported(*, is_causal: bool, seq_len: int, head_dim: int, num_q_heads: int, num_kv_heads: int,
+              dtype: torch.dtype = torch.bfloat16, kv_seq_len: int | None = None, batch: int = 1,
+              scale: float | None = None, causal_alignment: str = "top_left",
+              device: torch.device | int | None = None) -> bool:
+    """True iff the HIP kernels can serve this problem on this machine: the
+    library loads, the device (default: the current one) is a gfx950 GPU and
+    the sizes, dtype, mask and scale are ones the kernels take. The keyword
+    names and their meaning follow flash_hog/jax/_tk_gpu.py:70-80; kv_seq_len
+    (default seq_len), batch, dtype, scale (default head_dim ** -0.5) and
+    causal_alignment are the further arguments this library's limits depend on.
+    Nothing is launched or allocated."""
+    if causal_alignment not in ("top_left", "bottom_right"):
+        raise ValueError(f"causal_alignment must be 'top_left' or 'bottom_right', got {causal_alignment!r}")
+    try:
+        if device is None:
+            if not torch.cuda.is_available():
+                return False
+            device = torch.cuda.current_device()
+        index = device if isinstance(device, int) else torch.device(device).index
+        if index is None:
+            index = torch.cuda.current_device()
+        mask = (MaskType.NO_MASK if not is_causal else
+                MaskType.CAUSAL if causal_alignment == "top_left" else MaskType.CAUSAL_BOTTOM_RIGHT)
+        ok, _ = _hip.attention_supported(batch, seq_len, seq_len if kv_seq_len is None else kv_seq_len, num_q_heads,
+                                         num_kv_heads, head_dim, dtype, causal_code(mask),
+                                         head_dim ** -0.5 if scale is None else scale, device=index)
+        return ok
+    except (ImportError, OSError):
+        return False

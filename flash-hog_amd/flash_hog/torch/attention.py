@@ -59,7 +59,8 @@ def dot_product_attention(query, key, value, is_causal: bool = False, scale: flo
     unbatched = query.ndim == 3
     if unbatched:
         query, key, value = query.unsqueeze(0), key.unsqueeze(0), value.unsqueeze(0)
-    result, _ = _DotProductAttention.apply(query, key, value, mask_type, float(scale))
+    fn = _DotProductAttention if torch._C._are_functorch_transforms_active() else _DotProductAttentionEager
+    result, _ = fn.apply(query, key, value, mask_type, float(scale))
     if unbatched:
         result = result.squeeze(0)
     return result
@@ -100,7 +101,8 @@ class _DotProductAttention(torch.autograd.Function):
         # returns no cotangent for it); detaching it keeps this node out of the
         # graph of a second derivative, which would otherwise call it again with
         # a zero cotangent.
-        dq, dk, dv = _DotProductAttentionBwd.apply(ctx.mask_type, ctx.scale, q, k, v, activation, o.detach(), g)
+        fn = _DotProductAttentionBwd if torch._C._are_functorch_transforms_active() else _DotProductAttentionBwdEager
+        dq, dk, dv = fn.apply(ctx.mask_type, ctx.scale, q, k, v, activation, o.detach(), g)
         return dq, dk, dv, None, None
 
 
@@ -132,3 +134,29 @@ class _DotProductAttentionBwd(torch.autograd.Function):
         (dq2, dk2, dv2, _, _), ddo = attn_impl.dot_product_attention_bwd_rule_bwd_rule(
             mask_type=ctx.mask_type, scale=ctx.scale, res=res, g=(ddq, ddk, ddv))
         return None, None, dq2, dk2, dv2, None, None, ddo
+
+
+# The same two Functions in the ctx-first form. Function.apply binds a
+# setup_context-style Function's arguments through inspect.signature on every
+# call (tens of microseconds of host time, twice per Hessian-vector product);
+# the ctx-first form skips that. It cannot run under torch.func transforms, so
+# the callers above pick it only when none is active.
+
+class _DotProductAttentionEager(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, query, key, value, mask_type, scale):
+        output = _DotProductAttention.forward(query, key, value, mask_type, scale)
+        _DotProductAttention.setup_context(ctx, (query, key, value, mask_type, scale), output)
+        return output
+
+    backward = _DotProductAttention.backward
+
+
+class _DotProductAttentionBwdEager(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, mask_type, scale, query, key, value, activation, out, g):
+        output = _DotProductAttentionBwd.forward(mask_type, scale, query, key, value, activation, out, g)
+        _DotProductAttentionBwd.setup_context(ctx, (mask_type, scale, query, key, value, activation, out, g), output)
+        return output
+
+    backward = _DotProductAttentionBwd.backward

@@ -66,6 +66,19 @@ const char* fhog_status_string(int status);
 /* Message of the last failed call on this thread ("" if none). */
 const char* fhog_last_error(void);
 
+/*
+ * Whether this library has kernels for the given problem, without launching
+ * or allocating anything: FHOG_OK, or the status (with its fhog_last_error
+ * message) that the entry points would return for these sizes, dtype, causal
+ * and scale. device >= 0 also requires HIP device `device` to be a gfx950
+ * GPU (else FHOG_ERR_UNSUPPORTED); device < 0 checks the arguments only.
+ * Counterpart of the reference's supported() (flash_hog/jax/_tk_gpu.py:70-80),
+ * which answers the same question for its ThunderKittens kernels before a
+ * call, so that a caller can route unsupported shapes elsewhere.
+ */
+int fhog_attention_supported(int device, int batch, int n_q, int n_k, int heads, int kv_heads, int head_dim,
+                             int dtype, int causal, float scale);
+
 /* Bytes of fp32 row-statistic workspace per (delta, ddelta, bstat) array:
  * batch * heads * n_q * 4. */
 size_t fhog_row_stat_bytes(int batch, int heads, int n_q);

@@ -101,3 +101,66 @@ def fwd(q, k, v, scale, causal, heads=None):
         o[b, :, h, :], lse[b, h] = fwd_head(q[b, :, h, :].contiguous(), k[b, :, h, :].contiguous(),
                                             v[b, :, h, :].contiguous(), scale, causal)
     return o, lse
+
+
+# ------------------------------------------------- row-chunked (long sequences)
+#
+# The same equations with the (N_Q, N_K) matrices formed `rows` query rows at a
+# time, for sequences whose full matrices would not fit: every row statistic
+# (L, D, dD, B) and every query-side output (O, dQ2, ddO) depends on its own
+# rows only, and the key-side outputs (dK2, dV2) are sums over query rows, so
+# they accumulate chunk by chunk. A causal chunk of rows [r0, r1) needs keys
+# [0, r1) only (top-left mask, N_Q == N_K). Checked against the unchunked
+# functions in tests/test_gpu_parity.py::test_gpu_reference_chunked.
+
+def _chunk_keys(r1, n_k, causal):
+    return min(r1, n_k) if causal else n_k
+
+
+def fwd_head_chunked(q, k, v, scale, causal, rows=1024):
+    o = torch.empty((q.shape[0], v.shape[1]), device=q.device)
+    lse = torch.empty(q.shape[0], device=q.device)
+    for r0 in range(0, q.shape[0], rows):
+        r1 = min(r0 + rows, q.shape[0])
+        nk = _chunk_keys(r1, k.shape[0], causal)
+        s = torch.mm(q[r0:r1], k[:nk].t().contiguous()) * scale
+        if causal:
+            s = s.masked_fill(torch.arange(nk, device=q.device)[None, :] > torch.arange(r0, r1, device=q.device)[:, None],
+                              float("-inf"))
+        lse[r0:r1] = torch.logsumexp(s, dim=-1)
+        o[r0:r1] = torch.mm(torch.exp(s - lse[r0:r1, None]), v[:nk])
+        del s
+    return o, lse
+
+
+def bwdbwd_head_chunked(q, k, v, o, do, ddq, ddk, ddv, lse, scale, causal, rows=1024):
+    mm = torch.mm
+    dq2, ddo = torch.empty_like(q), torch.empty_like(do)
+    dk2, dv2 = torch.zeros_like(k), torch.zeros_like(v)
+    for r0 in range(0, q.shape[0], rows):
+        r1 = min(r0 + rows, q.shape[0])
+        nk = _chunk_keys(r1, k.shape[0], causal)
+        kc, vc, ddkc, ddvc = k[:nk], v[:nk], ddk[:nk], ddv[:nk]
+        qr, dor, ddqr = q[r0:r1], do[r0:r1], ddq[r0:r1]
+        s = mm(qr, kc.t().contiguous()) * scale
+        if causal:
+            s = s.masked_fill(torch.arange(nk, device=q.device)[None, :] > torch.arange(r0, r1, device=q.device)[:, None],
+                              float("-inf"))
+        p = torch.exp(s - lse[r0:r1, None])
+        del s
+        dp = mm(dor, vc.t().contiguous())
+        dds = scale * (mm(ddqr, kc.t().contiguous()) + mm(qr, ddkc.t().contiguous()))
+        d = (o[r0:r1] * dor).sum(-1)
+        dd = (dds * p).sum(-1)
+        dp2 = mm(dor, ddvc.t().contiguous()) - dp * dd[:, None] - dds * d[:, None] + dp * dds
+        b = (dp2 * p).sum(-1)
+        ds = scale * p * (dp - d[:, None])
+        ds2 = scale * p * (dp2 - b[:, None])
+        ddp = p * (dds - dd[:, None])
+        del dp, dp2, dds
+        dq2[r0:r1] = mm(ds, ddkc) + mm(ds2, kc)
+        ddo[r0:r1] = mm(p, ddvc) + mm(ddp, vc)
+        dk2[:nk] += mm(ds.t().contiguous(), ddqr) + mm(ds2.t().contiguous(), qr)
+        dv2[:nk] += mm(ddp.t().contiguous(), dor)
+        del p, ds, ds2, ddp
+    return dq2, dk2, dv2, ddo

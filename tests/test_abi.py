@@ -47,7 +47,7 @@ def test_python_signatures_cover_the_header():
 
 
 def test_status_strings(lib):
-    assert lib.fhog_abi_version() == 102
+    assert lib.fhog_abi_version() == 103
     assert lib.fhog_status_string(0) == b"ok"
     assert lib.fhog_status_string(1) == b"invalid argument"
     assert lib.fhog_status_string(2) == b"unsupported"
@@ -159,3 +159,47 @@ def test_library_imports_no_allocating_hip_routine():
     assert imported, out
     allocating = {n for n in imported if re.search(r"Malloc|Free|Alloc|HostRegister|MemPool", n)}
     assert not allocating, sorted(allocating)
+
+
+@pytest.mark.parametrize("kwargs,status,needle", [
+    (dict(), 0, ""),
+    (dict(head_dim=128, n_q=77, n_k=300, causal=2), 0, ""),
+    (dict(dtype=0), 0, ""),
+    (dict(heads=8, kv_heads=2, scale=-0.3), 0, ""),
+    (dict(head_dim=96), 2, "head_dim must be 64 or 128"),
+    (dict(head_dim=128, dtype=0), 2, "fp32 supports head_dim 64"),
+    (dict(heads=3, kv_heads=2), 1, "multiple of kv_heads"),
+    (dict(scale=0.0), 2, "scale must be nonzero"),
+    (dict(n_q=0), 1, "sizes must be >= 1"),
+])
+def test_supported_answers_as_the_entry_points_would(lib, kwargs, status, needle):
+    """fhog_attention_supported (device -1: arguments only, no HIP call)
+    returns the status and message that the entry points give for the same
+    arguments."""
+    args = dict(batch=1, n_q=16, n_k=16, heads=1, kv_heads=1, head_dim=64, dtype=2, causal=1, scale=0.125)
+    args.update(kwargs)
+    st = lib.fhog_attention_supported(-1, *args.values())
+    assert st == status
+    assert needle in lib.fhog_last_error().decode()
+    if status:
+        assert lib.fhog_attention_bwdbwd(*_bwdbwd_args(**args)) == status
+
+
+def test_supported_python_api_without_gpu():
+    """Mirrors flash_hog/jax/_tk_gpu.py:70-80: keyword arguments, a bool, and
+    False on a machine with no gfx950 GPU (here: none at all)."""
+    import torch
+
+    import flash_hog
+    from flash_hog import _hip
+
+    kw = dict(is_causal=True, seq_len=2048, head_dim=64, num_q_heads=16, num_kv_heads=16)
+    if not torch.cuda.is_available():
+        assert flash_hog.supported(**kw) is False
+    assert _hip.attention_supported(4, 2048, 2048, 16, 16, 64, torch.bfloat16, True, 0.125) == (True, "")
+    ok, why = _hip.attention_supported(4, 2048, 2048, 16, 16, 96, torch.bfloat16, True, 0.125)
+    assert not ok and "head_dim must be 64 or 128" in why
+    ok, why = _hip.attention_supported(4, 2048, 2048, 16, 16, 64, torch.float64, True, 0.125)
+    assert not ok and "dtype" in why
+    with pytest.raises(ValueError, match="causal_alignment"):
+        flash_hog.supported(**kw, causal_alignment="diagonal")

@@ -152,3 +152,33 @@ def test_vmap_hvp_equals_folded_batch(cuda_device):
     ref = flash_hog.dot_product_attention(dev["q"], dev["k"][:B].repeat(V, 1, 1, 1), dev["v"][:B].repeat(V, 1, 1, 1),
                                           is_causal=True)
     assert torch.equal(out.flatten(0, 1), ref)
+
+
+@pytest.mark.parametrize("kw,expect", [
+    (dict(is_causal=True, seq_len=2048, head_dim=64, num_q_heads=16, num_kv_heads=16), True),
+    (dict(is_causal=False, seq_len=1000, head_dim=64, num_q_heads=12, num_kv_heads=4, dtype=torch.float16), True),
+    (dict(is_causal=True, seq_len=200, head_dim=128, num_q_heads=4, num_kv_heads=4, kv_seq_len=300,
+          causal_alignment="bottom_right"), True),
+    (dict(is_causal=True, seq_len=256, head_dim=96, num_q_heads=2, num_kv_heads=2), False),
+    (dict(is_causal=True, seq_len=256, head_dim=128, num_q_heads=2, num_kv_heads=2, dtype=torch.float32), False),
+    (dict(is_causal=True, seq_len=256, head_dim=64, num_q_heads=3, num_kv_heads=2), False),
+], ids=["bench", "gqa_f16", "d128_br", "d96", "f32_d128", "bad_groups"])
+def test_supported_agrees_with_a_call(kw, expect, cuda_device):
+    """flash_hog.supported (the reference's _tk_gpu.py:70-80 query) says True
+    exactly where the front-end's double backward runs."""
+    import flash_hog
+
+    assert flash_hog.supported(**kw) is expect
+    dtype = kw.get("dtype", torch.bfloat16)
+    gen = torch.Generator().manual_seed(1)
+    B, T, S = 1, kw["seq_len"], kw.get("kv_seq_len", kw["seq_len"])
+    mk = lambda n, h: torch.randn((B, n, h, kw["head_dim"]), generator=gen).to(cuda_device, dtype)
+    q, k, v = mk(T, kw["num_q_heads"]), mk(S, kw["num_kv_heads"]), mk(S, kw["num_kv_heads"])
+    do, ddq, ddk, ddv = torch.randn_like(q), torch.randn_like(q), torch.randn_like(k), torch.randn_like(v)
+    align = kw.get("causal_alignment", "top_left")
+    if expect:
+        fhog_bwd_bwd(q, k, v, do, ddq, ddk, ddv, kw["is_causal"], None, causal_alignment=align)
+        torch.cuda.synchronize()
+    else:
+        with pytest.raises((ValueError, RuntimeError)):
+            fhog_bwd_bwd(q, k, v, do, ddq, ddk, ddv, kw["is_causal"], None, causal_alignment=align)

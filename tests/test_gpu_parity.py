@@ -236,3 +236,24 @@ def test_gpu_reference_matches_oracle(cuda_device):
                                  *(to_np(x[n]) for n in ("ddq", "ddk", "ddv")), to_np(lse), scale, True)
     for a, r in zip(got, ref):
         assert rel_err(a, r) < 1e-4
+
+
+
+@pytest.mark.parametrize("causal", [True, False], ids=["causal", "noncausal"])
+def test_gpu_reference_chunked(causal, cuda_device):
+    """The row-chunked closed forms (used by bench.py's HVP tables at long
+    sequences) equal the unchunked ones pinned above, with a ragged last chunk."""
+    import gpu_reference
+
+    _announce(f"gpu_reference chunked causal={causal}")
+    x = make_inputs(1, 600, 600, 1, 64, F32, seed=9)
+    scale = default_scale(64)
+    h = {n: t[0, :, 0, :].contiguous().to(cuda_device) for n, t in x.items()}
+    o, lse = gpu_reference.fwd_head(h["q"], h["k"], h["v"], scale, causal)
+    o_c, lse_c = gpu_reference.fwd_head_chunked(h["q"], h["k"], h["v"], scale, causal, rows=128)
+    assert rel_err(o_c, o) < 1e-5 and rel_err(lse_c, lse) < 1e-6
+    args = (h["q"], h["k"], h["v"], o, h["do"], h["ddq"], h["ddk"], h["ddv"], lse, scale, causal)
+    ref = gpu_reference.bwdbwd_head(*args)
+    got = gpu_reference.bwdbwd_head_chunked(*args, rows=128)
+    for a, r in zip(got, ref):
+        assert rel_err(a, r) < 1e-5
