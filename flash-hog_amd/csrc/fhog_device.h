@@ -233,14 +233,20 @@ struct GroupCursor {
 //
 // The LDS destination goes in M0. It is an operand bound to that register
 // ("{m0}"), so the compiler itself writes M0 before the statement and knows
-// its value afterwards; the statement only reads M0. The s_nop is the one wait
-// state the hardware needs between an SALU write of M0 and an LDS DMA, which
-// the compiler's hazard check does not see inside inline assembly.
+// its value afterwards; the statement only reads M0.
+//
+// Wait states. The compiler's hazard check does not look inside inline
+// assembly, so each statement starts with the ones its operands need: one
+// between an SALU write of M0 and an LDS DMA, and five between a VALU write of
+// an SGPR and a vector-memory instruction that reads that SGPR. The second
+// arises whenever the compiler reloads a spilled SGPR of the scalar base with
+// v_readlane just before the statement; the load could then read the base's
+// previous contents (say, a saved exec mask) and fault. s_nop 4 gives five.
 
 // 16 bytes per lane, addressed as a uniform 64-bit base (SGPR pair) plus a
 // per-lane 32-bit byte offset.
 __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
                :
                : "v"(voff), "s"(sbase), "{m0}"(lds_byte_addr)
                : "memory");
@@ -256,7 +262,7 @@ __device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_byte_addr) {
 
 // 4 bytes per lane, addressed as a uniform base plus a per-lane byte offset.
 __device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
+  asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1"
                :
                : "v"(voff), "s"(sbase), "{m0}"(lds_byte_addr)
                : "memory");
