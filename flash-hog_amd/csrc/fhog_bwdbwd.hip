@@ -664,6 +664,7 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stage
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
+    if constexpr (sizeof(T) == 2 && D == 128) return launch_bwdbwd_stage2_k16<T, D, CAUSAL>(p, stream);
     // Pair causal key blocks when the grid outnumbers the resident workgroups.
     const int npairs = p.batch * p.kv_heads;
     const int resident = resident_workgroups(Occupancy<T, D>::value);

@@ -52,5 +52,8 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t s, int stages = 3
 // Stage 1 in one sweep (2-byte types); launch_bwdbwd selects it.
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd_stage1_fused(const BwdBwdParams<T>& p, hipStream_t s);
+// Stage 2 with 16 keys per wave (2-byte types, D = 128); launch_bwdbwd selects it.
+template <typename T, int D, bool CAUSAL>
+hipError_t launch_bwdbwd_stage2_k16(const BwdBwdParams<T>& p, hipStream_t s);
 
 }  // namespace fhog

@@ -62,6 +62,9 @@ SCALE_CASES = [
     ("bf16_causal_scale_-0.125", 1, 192, 192, 2, 2, 64, BF16, TL, -0.125),
     ("f16_noncausal_ragged_scale_-0.2", 1, 150, 150, 2, 2, 64, F16, NONE, -0.2),
     ("f16_d128_bottom_right_scale_-0.05", 1, 100, 160, 2, 1, 128, F16, BR, -0.05),
+    # power-of-two scales at D = 128 (both stages fold them into their resident operands)
+    ("bf16_d128_causal_scale_0.125", 1, 300, 300, 4, 2, 128, BF16, TL, 0.125),
+    ("bf16_d128_noncausal_ragged_scale_0.0625", 2, 150, 230, 2, 2, 128, BF16, NONE, 0.0625),
     ("f32_causal_scale_-0.125", 1, 96, 96, 2, 2, 64, F32, TL, -0.125),
 ]
 SCALE_IDS = [c[0] for c in SCALE_CASES]
