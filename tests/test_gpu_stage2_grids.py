@@ -1,6 +1,7 @@
 """The double backward on shapes that select each of stage 2's grid layouts.
 
-Stage 2 (pass 4, tiled over 128-key blocks) lays its grid out by the problem's
+Stage 2 (pass 4, tiled over key blocks: 128 keys at D = 64, 64 keys in the
+16-key-per-wave kernel used for 2-byte types at D = 128) lays its grid out by the problem's
 size: one key block per workgroup when the grid fits on the GPU at once; for
 larger causal grids a workgroup takes key block r and then its mirror
 nkb - 1 - r (odd nkb leaves the middle block alone); and when that paired grid
@@ -28,18 +29,26 @@ pytestmark = pytest.mark.gpu
 
 TOL = 2e-2
 
-# id, batch, n_q, n_k, heads, kv_heads, causal (C ABI code)
+# id, batch, n_q, n_k, heads, kv_heads, causal (C ABI code), head_dim
 SHAPES = [
     # 18 key blocks x 32 (batch, head) pairs > 512 resident workgroups: mirror pairs
-    ("mirror_pairs_even", 16, 2304, 2304, 2, 2, 1),
+    ("mirror_pairs_even", 16, 2304, 2304, 2, 2, 1, 64),
     # 17 key blocks: the middle block has no mirror
-    ("mirror_pairs_odd", 16, 2176, 2176, 2, 2, 1),
+    ("mirror_pairs_odd", 16, 2176, 2176, 2, 2, 1, 64),
     # grouped heads (4 query heads per key/value head) with mirror pairs
-    ("mirror_pairs_gqa4", 8, 2304, 2304, 16, 4, 1),
+    ("mirror_pairs_gqa4", 8, 2304, 2304, 16, 4, 1, 64),
     # top-left causal, N_K > N_Q: key blocks past N_Q see no query (empty blocks in pairs)
-    ("mirror_pairs_empty_blocks", 16, 1024, 2304, 2, 2, 1),
+    ("mirror_pairs_empty_blocks", 16, 1024, 2304, 2, 2, 1, 64),
     # bottom-right causal with N_Q > N_K
-    ("mirror_pairs_bottom_right", 16, 2600, 2304, 2, 2, 2),
+    ("mirror_pairs_bottom_right", 16, 2600, 2304, 2, 2, 2, 64),
+    # D = 128 (64-key blocks): 32 blocks x 32 pairs, paired grid of exactly 512: skewed pairs
+    ("d128_skewed_pairs", 16, 2048, 2048, 2, 2, 1, 128),
+    # 33 blocks: mirror pairs, the middle block alone
+    ("d128_mirror_pairs_odd", 16, 2112, 2112, 2, 2, 1, 128),
+    # grouped heads, bottom-right causal with N_Q > N_K, mirror pairs
+    ("d128_gqa4_bottom_right", 4, 2600, 2304, 16, 4, 2, 128),
+    # top-left causal, N_K > N_Q: empty key blocks in pairs
+    ("d128_empty_blocks", 16, 1024, 2304, 2, 2, 1, 128),
 ]
 
 
@@ -96,9 +105,9 @@ def _bwdbwd_head(q, k, v, o, do, ddq, ddk, ddv, lse, scale, causal):
 def test_stage2_grid_layouts(shape, cuda_device):
     from flash_hog import _hip
 
-    name, B, Nq, Nk, H, Hk, causal = shape
+    name, B, Nq, Nk, H, Hk, causal, D = shape
     print("[case] stage-2 grid", name, flush=True)
-    dtype, D = torch.bfloat16, 64
+    dtype = torch.bfloat16
     scale = 1.0 / math.sqrt(D)
     x = make_inputs(B, Nq, Nk, H, D, dtype, seed=71, kv_heads=Hk, device=cuda_device)
     o, lse = _reference_residual(x, scale, causal, dtype)
