@@ -47,7 +47,7 @@ struct Scores16 {
 template <typename T, int D, bool CAUSAL, bool PRE>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(2, 2)))
-bwdbwd_k16_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
+bwdbwd_k16_kernel(BwdBwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 32;             // 32-deep steps over the head dim (score products)
   constexpr int DB = D / 16;             // 16-wide output column blocks
@@ -68,17 +68,14 @@ bwdbwd_k16_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
   const int n = lane & 15, g = lane >> 4;
   const int nbh = p.batch * p.kv_heads;
   const int nkb = (p.nk + BKB - 1) / BKB;
-  // Key block `rank` of pair bh, longest first; with pairs >= 1 also the
-  // mirror block (fhog_bwdbwd.hip's stage 2 describes the pairing and skew).
-  const GridSlot slot = grid_slot(blockIdx.x, nbh, pairs ? (nkb + 1) / 2 : nkb, chunk);
+  // Key block `rank` of pair bh, the longest (causal) first. Unlike the 32-key
+  // kernel, this one does not pair key block r with its mirror: its grids have
+  // twice as many blocks, and rank-major order balances them better (stage 2
+  // at B2 N8192 H16 D128: 2.54-2.57 ms unpaired against 2.64 ms paired).
+  const GridSlot slot = grid_slot(blockIdx.x, nbh, nkb, chunk);
   const int bh = slot.pair;
-  const int first = slot.rank;
-  int second = nkb - 1 - slot.rank;
-  if (pairs == 2) second += slot.rank < nkb / 4 ? -(nkb / 4) : nkb / 4;
-  const int nblk = (pairs && second != first) ? 2 : 1;
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int kb = blk == 0 ? first : second;
-    if (blk > 0) __syncthreads();  // every wave is done with the previous block's ring
+  {
+    const int kb = slot.rank;
     const int b = bh / p.kv_heads, hk = bh % p.kv_heads;
     const int grp = p.heads / p.kv_heads;  // query heads per key/value head
     const long rs = (long)p.heads * D;      // query-side row stride
@@ -339,20 +336,14 @@ hipError_t launch_bwdbwd_stage2_k16(const BwdBwdParams<T>& p, hipStream_t stream
   static_assert(sizeof(T) == 2, "2-byte types only");
   const int nkb = (p.nk + kKeys * kWaves - 1) / (kKeys * kWaves);
   const int npairs = p.batch * p.kv_heads;
-  const int resident = resident_workgroups(2);
-  // The pairing and skew of fhog_bwdbwd.hip's stage 2.
-  int pairs = CAUSAL && nkb * npairs > resident;
-  const int nranks = pairs ? (nkb + 1) / 2 : nkb;
-  if (pairs && nkb % 4 == 0 && nranks * npairs == resident) pairs = 2;
-  const int chunk = grid_chunk(npairs, nranks, resident);
-  const dim3 grid(nranks * npairs);
+  const int chunk = grid_chunk(npairs, nkb, resident_workgroups(2));
+  const dim3 grid(nkb * npairs);
   int e2;
   if (std::is_same_v<T, __bf16> && std::frexp(p.scale, &e2) == 0.5f)  // scale = 2^(e2 - 1)
     hipLaunchKernelGGL((bwdbwd_k16_kernel<T, D, CAUSAL, std::is_same_v<T, __bf16>>), grid, dim3(kThreads), 0,
-                       stream, p, pairs, chunk);
+                       stream, p, chunk);
   else
-    hipLaunchKernelGGL((bwdbwd_k16_kernel<T, D, CAUSAL, false>), grid, dim3(kThreads), 0, stream, p, pairs,
-                       chunk);
+    hipLaunchKernelGGL((bwdbwd_k16_kernel<T, D, CAUSAL, false>), grid, dim3(kThreads), 0, stream, p, chunk);
   return hipGetLastError();
 }
 

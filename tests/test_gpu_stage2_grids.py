@@ -1,7 +1,8 @@
 """The double backward on shapes that select each of stage 2's grid layouts.
 
 Stage 2 (pass 4, tiled over key blocks: 128 keys at D = 64, 64 keys in the
-16-key-per-wave kernel used for 2-byte types at D = 128) lays its grid out by the problem's
+16-key-per-wave kernel used for 2-byte types at D = 128, which keeps plain
+rank-major or chunked order) lays its grid out by the problem's
 size: one key block per workgroup when the grid fits on the GPU at once; for
 larger causal grids a workgroup takes key block r and then its mirror
 nkb - 1 - r (odd nkb leaves the middle block alone); and when that paired grid
@@ -41,14 +42,16 @@ SHAPES = [
     ("mirror_pairs_empty_blocks", 16, 1024, 2304, 2, 2, 1, 64),
     # bottom-right causal with N_Q > N_K
     ("mirror_pairs_bottom_right", 16, 2600, 2304, 2, 2, 2, 64),
-    # D = 128 (64-key blocks): 32 blocks x 32 pairs, paired grid of exactly 512: skewed pairs
-    ("d128_skewed_pairs", 16, 2048, 2048, 2, 2, 1, 128),
-    # 33 blocks: mirror pairs, the middle block alone
-    ("d128_mirror_pairs_odd", 16, 2112, 2112, 2, 2, 1, 128),
-    # grouped heads, bottom-right causal with N_Q > N_K, mirror pairs
+    # D = 128 (64-key blocks, no mirror pairs): 32 blocks x 32 pairs, rank-major
+    ("d128_rank_major", 16, 2048, 2048, 2, 2, 1, 128),
+    # 33 blocks, the last one ragged
+    ("d128_ragged_last_block", 16, 2100, 2100, 2, 2, 1, 128),
+    # grouped heads, bottom-right causal with N_Q > N_K
     ("d128_gqa4_bottom_right", 4, 2600, 2304, 16, 4, 2, 128),
-    # top-left causal, N_K > N_Q: empty key blocks in pairs
+    # top-left causal, N_K > N_Q: key blocks no query sees
     ("d128_empty_blocks", 16, 1024, 2304, 2, 2, 1, 128),
+    # 16 blocks x 288 pairs = 9 rounds of 512 workgroups: chunked grid order
+    ("d128_chunked", 144, 1024, 1024, 2, 2, 1, 128),
 ]
 
 
