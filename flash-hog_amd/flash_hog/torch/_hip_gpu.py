@@ -206,7 +206,8 @@ def supported(*, is_causal: bool, seq_len: int, head_dim: int, num_q_heads: int,
     names and their meaning follow flash_hog/jax/_tk_gpu.py:70-80; kv_seq_len
     (default seq_len), batch, dtype, scale (default head_dim ** -0.5) and
     causal_alignment are the further arguments this library's limits depend on.
-    Nothing is launched or allocated."""
+    Head dims that dot_product_attention zero-pads to one the kernels take
+    count as supported. Nothing is launched or allocated."""
     if causal_alignment not in ("top_left", "bottom_right"):
         raise ValueError(f"causal_alignment must be 'top_left' or 'bottom_right', got {causal_alignment!r}")
     try:
@@ -219,9 +220,13 @@ def supported(*, is_causal: bool, seq_len: int, head_dim: int, num_q_heads: int,
             index = torch.cuda.current_device()
         mask = (MaskType.NO_MASK if not is_causal else
                 MaskType.CAUSAL if causal_alignment == "top_left" else MaskType.CAUSAL_BOTTOM_RIGHT)
+        from flash_hog.torch.attention import kernel_head_dim
+
+        kernel_dim = kernel_head_dim(dtype, head_dim) if head_dim >= 1 else None
         ok, _ = _hip.attention_supported(batch, seq_len, seq_len if kv_seq_len is None else kv_seq_len, num_q_heads,
-                                         num_kv_heads, head_dim, dtype, causal_code(mask),
-                                         head_dim ** -0.5 if scale is None else scale, device=index)
+                                         num_kv_heads, head_dim if kernel_dim is None else kernel_dim, dtype,
+                                         causal_code(mask), head_dim ** -0.5 if scale is None else scale,
+                                         device=index)
         return ok
     except (ImportError, OSError):
         return False

@@ -29,6 +29,23 @@ from flash_hog._types import MaskType
 from flash_hog.torch import _attention_impl as attn_impl
 
 
+# Head dims the kernels take, per dtype. Another head dim up to the largest is
+# served by zero-padding q, k and v to the next one: padded columns add nothing
+# to any score, give zero output columns, and their gradients are dropped by the
+# padding's own backward, so the results are those of the unpadded problem (at
+# the cost of the copies and of the padded columns' arithmetic).
+_KERNEL_HEAD_DIMS = {torch.bfloat16: (64, 128), torch.float16: (64, 128), torch.float32: (64,)}
+
+
+def kernel_head_dim(dtype, head_dim: int) -> int | None:
+    """The head dim the kernels compute a problem of this head dim in (itself or
+    the padded one), or None if none takes it."""
+    for d in _KERNEL_HEAD_DIMS.get(dtype, ()):
+        if head_dim <= d:
+            return d
+    return None
+
+
 def dot_product_attention(query, key, value, is_causal: bool = False, scale: float | None = None, *,
                           causal_alignment: str = "top_left"):
     """Softmax attention over (B, T, N, H) or unbatched (T, N, H) tensors.
@@ -42,9 +59,20 @@ def dot_product_attention(query, key, value, is_causal: bool = False, scale: flo
     causal diagonal: "top_left" (key s visible to query t iff s <= t, the
     reference kernel's mask) or "bottom_right" (s <= t + S - T, the mask of
     flash_hog/_jax_refs/jax_impl.py:104-109); they agree when T == S.
+
+    Like the reference's kernel, any head dim H >= 1 works up to the largest
+    one the kernels take (128 for bf16 and fp16, 64 for fp32); head dims the
+    kernels do not take natively are zero-padded to the next one they do.
     """
     if scale is None:
         scale = query.shape[-1] ** -0.5
+    head_dim = query.shape[-1]
+    padded = kernel_head_dim(query.dtype, head_dim)
+    if padded is not None and padded != head_dim and key.shape[-1] == value.shape[-1] == head_dim:
+        pad = lambda t: torch.nn.functional.pad(t, (0, padded - head_dim))
+        out = dot_product_attention(pad(query), pad(key), pad(value), is_causal, scale,
+                                    causal_alignment=causal_alignment)
+        return out[..., :head_dim]
     dtype = query.dtype
     if not (dtype == key.dtype == value.dtype):
         raise ValueError(f"query, key and value must share a dtype, got {query.dtype}, {key.dtype}, {value.dtype}")

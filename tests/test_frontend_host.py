@@ -82,3 +82,23 @@ def test_grad_of_grad_stops_at_second_order():
 def test_unbatched_shapes():
     q, k = meta(64, 4, 64), meta(80, 2, 64)
     assert attn(q, k, k).shape == q.shape
+
+
+def test_padded_head_dims_keep_shapes():
+    """Head dims the kernels do not take natively are zero-padded to 64 or 128
+    and sliced back; the derivatives keep the caller's shapes."""
+    from flash_hog.torch.attention import kernel_head_dim
+
+    assert kernel_head_dim(torch.bfloat16, 96) == 128 and kernel_head_dim(torch.bfloat16, 1) == 64
+    assert kernel_head_dim(torch.float16, 128) == 128 and kernel_head_dim(torch.bfloat16, 129) is None
+    assert kernel_head_dim(torch.float32, 48) == 64 and kernel_head_dim(torch.float32, 96) is None
+    q = meta(2, 16, 4, 96).requires_grad_(True)
+    k = meta(2, 16, 2, 96).requires_grad_(True)
+    v = meta(2, 16, 2, 96).requires_grad_(True)
+    out = attn(q, k, v)
+    assert out.shape == q.shape
+    g = torch.autograd.grad(out, (q, k, v), torch.empty_like(out), create_graph=True)
+    h = torch.autograd.grad(g, (q, k, v), tuple(torch.empty_like(t) for t in g))
+    assert [t.shape for t in h] == [q.shape, k.shape, v.shape]
+    out = torch.func.vmap(attn)(meta(3, 2, 16, 4, 40), meta(3, 2, 16, 4, 40), meta(3, 2, 16, 4, 40))
+    assert out.shape == (3, 2, 16, 4, 40)

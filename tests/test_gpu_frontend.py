@@ -48,6 +48,34 @@ def test_backward_backward_single(is_causal, dtype, cuda_device):
         assert rel_err(a, r) < TOL[dtype], n
 
 
+@pytest.mark.parametrize("head_dim,dtype,is_causal", [
+    (32, torch.bfloat16, True), (80, torch.bfloat16, False), (96, torch.float16, True),
+    (16, torch.bfloat16, True), (40, torch.float32, True),
+], ids=["d32_bf16_causal", "d80_bf16", "d96_f16_causal", "d16_bf16_causal", "d40_f32_causal"])
+def test_padded_head_dims(head_dim, dtype, is_causal, cuda_device):
+    """Head dims the kernels do not take natively (the reference's kernel has no
+    head-dim limit, flash_hog/jax/_pallas_gpu_kernel.py:80-101) run zero-padded
+    to 64 or 128: forward, first and second derivatives against the fp64
+    autodiff oracle, at the unpadded head dim's default scale."""
+    print("[case] frontend padded head dim", head_dim, dtype, is_causal, flush=True)
+    x = make_inputs(2, 150, 150, 2, head_dim, dtype, seed=61)
+    scale = default_scale(head_dim)
+    dev = {n: t.to(cuda_device) for n, t in x.items()}
+    (dq2, dk2, dv2, ddo), (out, dq, dk, dv) = fhog_bwd_bwd(
+        dev["q"], dev["k"], dev["v"], dev["do"], dev["ddq"], dev["ddk"], dev["ddv"], is_causal, None)
+    torch.cuda.synchronize()
+    assert out.shape == dev["q"].shape and dq2.shape == dev["q"].shape
+    c = {n: t.double() for n, t in x.items()}
+    ref2 = autodiff.double_vjp(c["q"], c["k"], c["v"], c["do"], c["ddq"], c["ddk"], c["ddv"], scale, is_causal)
+    ref1 = autodiff.first_vjp(c["q"], c["k"], c["v"], c["do"], scale, is_causal)
+    ref_out = autodiff.attention(c["q"], c["k"], c["v"], scale, is_causal)
+    assert rel_err(out, ref_out) < TOL[dtype]
+    for a, r, n in zip((dq, dk, dv), ref1, ("dq", "dk", "dv")):
+        assert rel_err(a, r) < TOL[dtype], n
+    for a, r, n in zip((dq2, dk2, dv2, ddo), ref2, ("dq2", "dk2", "dv2", "ddo")):
+        assert rel_err(a, r) < TOL[dtype], n
+
+
 def test_unbatched_inputs(cuda_device):
     """(T, N, H) inputs get a batch axis added and removed (attention.py:39-47)."""
     import flash_hog
@@ -159,10 +187,11 @@ def test_vmap_hvp_equals_folded_batch(cuda_device):
     (dict(is_causal=False, seq_len=1000, head_dim=64, num_q_heads=12, num_kv_heads=4, dtype=torch.float16), True),
     (dict(is_causal=True, seq_len=200, head_dim=128, num_q_heads=4, num_kv_heads=4, kv_seq_len=300,
           causal_alignment="bottom_right"), True),
-    (dict(is_causal=True, seq_len=256, head_dim=96, num_q_heads=2, num_kv_heads=2), False),
+    (dict(is_causal=True, seq_len=256, head_dim=96, num_q_heads=2, num_kv_heads=2), True),
+    (dict(is_causal=True, seq_len=256, head_dim=160, num_q_heads=2, num_kv_heads=2), False),
     (dict(is_causal=True, seq_len=256, head_dim=128, num_q_heads=2, num_kv_heads=2, dtype=torch.float32), False),
     (dict(is_causal=True, seq_len=256, head_dim=64, num_q_heads=3, num_kv_heads=2), False),
-], ids=["bench", "gqa_f16", "d128_br", "d96", "f32_d128", "bad_groups"])
+], ids=["bench", "gqa_f16", "d128_br", "d96_padded", "d160", "f32_d128", "bad_groups"])
 def test_supported_agrees_with_a_call(kw, expect, cuda_device):
     """flash_hog.supported (the reference's _tk_gpu.py:70-80 query) says True
     exactly where the front-end's double backward runs."""
