@@ -21,6 +21,14 @@
 // sum P u K, sum P K, ddO part). The dP accumulator starts at -D, so it ends
 // as u.
 //
+// Rows that see exactly one key (the first row of a causal problem, or every
+// row when N_K = 1). There P = 1, dS = dS2 = ddP = 0, so dQ2 = 0 and ddO =
+// ddV_0 exactly, while the sums above cancel only up to the bf16 rounding of
+// X and x (about 1e-2 at unit-size inputs where the exact value is 0). The
+// epilogue writes dQ2 = 0 for such rows and subtracts bf16(dD) O instead of
+// dD O from the ddO accumulator: with one key, x = dD and O = V_0, so that
+// cancels the rounding of x exactly, and c = <dO, ddO> and B follow exactly.
+//
 // Sixteen queries per wave. The five accumulators of 32 queries would not fit
 // beside the score tiles in the 256 registers of a wave that shares its SIMD
 // with another, and two co-resident waves are what overlaps one wave's matrix
@@ -302,6 +310,9 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   }
 
   const float dD = group4_sum(dd_acc);
+  // A row that sees exactly one key (see above).
+  const bool one_key = (CAUSAL ? min(p.nk, qi + p.coff + 1) : p.nk) == 1;
+  const float dDo = one_key ? (float)(T)dD : dD;  // the dD that multiplies O in ddO
   // ddO = acc_o - dD O and c = <dO, ddO>, from this lane's four columns of
   // each 16-column block (16 db + 4 g + i), summed over the four lane groups.
   const long roff = qbase + (long)qi * rs;
@@ -320,7 +331,7 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      y[db][i] = acc_o[db][i] - dD * (float)ov[i];
+      y[db][i] = acc_o[db][i] - dDo * (float)ov[i];
       cpart = fmaf((float)dov[i], y[db][i], cpart);
     }
   }
@@ -339,7 +350,8 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
       const int d = 16 * db + 4 * g;  // this lane's four output columns
       f32x4 x;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[i] = scale * (acc_a[db][i] - dD * acc_s[db][i] - c * acc_p[db][i]);
+      for (int i = 0; i < 4; ++i)
+        x[i] = one_key ? 0.f : scale * (acc_a[db][i] - dD * acc_s[db][i] - c * acc_p[db][i]);
       *reinterpret_cast<V4<T>*>(dq2 + d) = cvt4<T>(x);
       *reinterpret_cast<V4<T>*>(ddo + d) = cvt4<T>(y[db]);
     }
