@@ -309,6 +309,9 @@ bwdbwd_q_kernel(BwdBwdParams<T> p, int chunk) {
   if (qvalid) {
     T* dq2 = p.dq2 + qbase + (long)qi * rs;
     T* ddo = p.ddo + qbase + (long)qi * rs;
+    // A row that sees exactly one key has a constant softmax: its dQ2 is
+    // exactly 0, while the sums above cancel only to rounding of c.
+    const bool one_key = (CAUSAL ? min(p.nk, qi + p.coff + 1) : p.nk) == 1;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
@@ -317,7 +320,7 @@ bwdbwd_q_kernel(BwdBwdParams<T> p, int chunk) {
         f32x4 x, y;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          x[j] = acc_dq2[dt][4 * a + j] * scale;
+          x[j] = one_key ? 0.f : acc_dq2[dt][4 * a + j] * scale;
           y[j] = acc_ddo[dt][4 * a + j];
         }
         *reinterpret_cast<V4<T>*>(dq2 + d) = cvt4<T>(x);
@@ -390,6 +393,7 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
     const int k0 = kb * BKB + wave * 32;
     const int kj = k0 + n;
     const bool kvalid = kj < p.nk;
+    const int qfirst = first_contributing_query(p, kj, CAUSAL);
 
     // Iteration i visits query tile qt_begin + i / grp of query head
     // hk * grp + i % grp (the group reduction of
@@ -581,10 +585,10 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
           f32x16 P;
   #pragma unroll
           for (int r = 0; r < 16; ++r) P[r] = exp2_fast(S[r] * c2);
-          const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31 - p.coff);
+          const bool need_mask = (q0 + BQ > p.nq) || (CAUSAL && q0 < k0 + 31 - p.coff) || p.nk == 1;
           if (need_mask) {
-            // visible iff query >= key - coff (causal) and query < nq
-            const int qlo = (CAUSAL ? kj - p.coff : 0) - q0, qhi = p.nq - q0;
+            // a pair enters iff qfirst <= query < nq
+            const int qlo = qfirst - q0, qhi = p.nq - q0;
   #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int m = crow(r, g);

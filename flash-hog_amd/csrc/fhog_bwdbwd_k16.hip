@@ -86,6 +86,7 @@ bwdbwd_k16_kernel(BwdBwdParams<T> p, int chunk) {
     const int k0 = kb * BKB + wave * kKeys;
     const int kj = k0 + n;
     const bool kvalid = kj < p.nk;
+    const int qfirst = first_contributing_query(p, kj, CAUSAL);
 
     // Iteration i visits query tile qt_begin + i / grp of query head
     // hk * grp + i % grp (the group reduction of _pallas_gpu_kernel.py:333-370).
@@ -269,7 +270,7 @@ bwdbwd_k16_kernel(BwdBwdParams<T> p, int chunk) {
       auto finish = [&](int i, const Scores16& sc, const Iter& it, auto mask_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
         const uint32_t sa = slot_addr(i);
-        const int qlo = (CAUSAL ? kj - p.coff : 0) - it.q0, qhi = p.nq - it.q0;
+        const int qlo = qfirst - it.q0, qhi = p.nq - it.q0;
         f32x8 vS, vS2, vP;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {

@@ -44,6 +44,19 @@ template <typename T> struct BwdBwdParams {
   float scale;
 };
 
+// First query row whose pair with key kj enters dK2 and dV2. A query that
+// sees no key but kj has a constant softmax (P = 1 whatever Q, K, V), so the
+// pair's terms dS, dS2, ddP are exactly zero, while their fp32 forms cancel
+// only to the rounding of the row statistics (about 1e-7 of |D dD| + |B|).
+// Stage 2 drops such pairs as it drops masked ones: every row when nk = 1,
+// else, under the causal mask, row -coff for key 0; rows before
+// kj - coff do not see kj at all.
+template <typename T>
+__device__ inline int first_contributing_query(const BwdBwdParams<T>& p, int kj, bool causal) {
+  if (p.nk == 1) return p.nq;
+  return causal ? kj - p.coff + (kj == 0) : 0;
+}
+
 template <typename T, int D, bool CAUSAL> hipError_t launch_fwd(const FwdParams<T>& p, hipStream_t s);
 template <typename T, int D, bool CAUSAL> hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t s);
 // stages: bit 0 = stage 1 (passes 1-3), bit 1 = stage 2 (pass 4).
