@@ -199,6 +199,15 @@ def hvp_table(args):
                                                    scale=scale).float()
         return f
 
+    def attn_standin(dtype):
+        """The HVP's function with attention replaced by an element-wise
+        product (same casts, same autograd graph depth, no kernel of this
+        library): its eager HVP time is the host-time floor of the eager
+        column at short sequences, where the GPU work is shorter than the host's."""
+        def f(q, k, v):
+            return (q.to(dtype) * k.to(dtype) * v.to(dtype)).float()
+        return f
+
     def attn_dense(q, k, v):
         qh, kh, vh = (t.permute(0, 2, 1, 3).contiguous() for t in (q, k, v))
         s = torch.matmul(qh, kh.transpose(-1, -2).contiguous()) * scale
@@ -218,6 +227,18 @@ def hvp_table(args):
         x = [t.detach().requires_grad_(True) for t in x]
         g = torch.autograd.grad(attn(*x), x, cot, create_graph=True)
         return torch.autograd.grad(g, x, tan)
+
+    def eager_ms(f, x, cot, tan, iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(2):
+            out = hvp(f, x, cot, tan)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            out = hvp(f, x, cot, tan)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters, out
 
     def graph_ms(f, x, cot, tan, iters):
         """Mean replay time of the HVP captured in a HIP graph (torch.cuda.graph)."""
@@ -266,8 +287,8 @@ def hvp_table(args):
 
     rows = []
     settled = False
-    log("| batch | seq | HVP (ms) | HVP, graph replay (ms) | faithfulness |")
-    log("|--:|--:|--:|--:|:--|")
+    log("| batch | seq | HVP (ms) | HVP, graph replay (ms) | host floor (ms) | faithfulness |")
+    log("|--:|--:|--:|--:|--:|:--|")
     for B, N in HVP_TABLES[args.hvp_table]:
         gen = torch.Generator().manual_seed(B * 7919 + N)
         mk = lambda: torch.randn((B, N, H, D), generator=gen).to(dev)
@@ -277,17 +298,9 @@ def hvp_table(args):
         if not settled:
             settle(torch, lambda: hvp(f, x, cot, tan), args.settle_ms, batch=1)
             settled = True
-        for _ in range(2):
-            out = hvp(f, x, cot, tan)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(iters):
-            out = hvp(f, x, cot, tan)
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / iters
+        ms, out = eager_ms(f, x, cot, tan, iters)
         gms = graph_ms(f, x, cot, tan, iters) if N <= GRAPH_MAX_SEQ else None
+        floor_ms = eager_ms(attn_standin(torch.bfloat16), x, cot, tan, iters)[0] if N <= GRAPH_MAX_SEQ else None
         if B * N * N <= 2048 * 2048:
             ref, against = hvp(attn_dense, x, cot, tan), "dense fp32"
         else:
@@ -296,14 +309,16 @@ def hvp_table(args):
             out = [t[b, :, h, :] for b, h in slices for t in out]
         faith = "not measured"
         row = {"table": args.hvp_table, "batch": B, "seq": N, "heads": H, "head_dim": D, "hvp_ms": round(ms, 4),
-               "hvp_graph_ms": None if gms is None else round(gms, 4), "iterations": iters}
+               "hvp_graph_ms": None if gms is None else round(gms, 4),
+               "host_floor_ms": None if floor_ms is None else round(floor_ms, 4), "iterations": iters}
         if ref is not None:
             cos, rel = compare(out, ref)
             faith = f"cos {cos:.4f}, max rel err {rel:.1e} vs {against}"
             row.update(cos=round(cos, 6), max_rel_err=rel, against=against)
         torch.cuda.synchronize()
         gtxt = "-" if gms is None else f"{gms:.2f}"
-        log(f"| {B} | {N} | {ms:.2f} | {gtxt} | {faith} |")
+        ftxt = "-" if floor_ms is None else f"{floor_ms:.2f}"
+        log(f"| {B} | {N} | {ms:.2f} | {gtxt} | {ftxt} | {faith} |")
         print(json.dumps(row), flush=True)
         rows.append(row)
         del x, cot, tan, out, ref

@@ -1,10 +1,15 @@
-"""Build libflash_hog_hip.so (the C-ABI kernel library) for gfx950 with hipcc.
+"""Build libflash_hog_hip.so (the C-ABI kernel library) for gfx950 with hipcc,
+and the torch extension that calls it from C++ (_fhog_torch).
 
 Usage: python flash-hog_amd/build.py [--jobs N] [--out DIR]
 
 Each .hip source under csrc/ is compiled to an object in parallel, then the
 objects are linked into flash_hog/_lib/libflash_hog_hip.so next to the Python
-package that loads it. hipcc cross-compiles without a GPU.
+package that loads it. hipcc cross-compiles without a GPU. csrc/fhog_torch.cpp
+is compiled with g++ against the installed torch's headers into
+flash_hog/_lib/_fhog_torch<ext suffix>: tensor-level calls of the C ABI that
+flash_hog/_hip.py prefers to its Python wrappers (less host time per call). It
+links no kernel code; it calls the entry points of the library _hip.py loaded.
 """
 
 from __future__ import annotations
@@ -77,13 +82,51 @@ def build(jobs: int | None = None, out_dir: pathlib.Path | None = None) -> pathl
     return lib
 
 
+TORCH_EXT_SRC = CSRC / "fhog_torch.cpp"
+TORCH_EXT_NAME = "_fhog_torch"
+
+
+def build_torch_ext(out_dir: pathlib.Path | None = None) -> pathlib.Path:
+    """Compiles csrc/fhog_torch.cpp into a Python extension module for the
+    installed torch (ROCm build) and this interpreter."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    out_dir = pathlib.Path(out_dir) if out_dir else LIB_DIR
+    out_dir.mkdir(parents=True, exist_ok=True)
+    lib_dirs = cpp_extension.library_paths()
+    out = out_dir / (TORCH_EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = [
+        shutil.which("g++") or "g++", "-O2", "-std=c++17", "-shared", "-fPIC",
+        f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+        f"-DTORCH_EXTENSION_NAME={TORCH_EXT_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+        "-D__HIP_PLATFORM_AMD__", "-DUSE_ROCM",
+        *[f"-I{p}" for p in cpp_extension.include_paths()],
+        f"-I{sysconfig.get_paths()['include']}", "-I/opt/rocm/include", f"-I{REPO / 'include'}",
+        str(TORCH_EXT_SRC), "-o", str(tmp),
+        *[f"-L{p}" for p in lib_dirs], *[f"-Wl,-rpath,{p}" for p in lib_dirs],
+        "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+    ]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed for {TORCH_EXT_SRC.name}:\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--out", type=pathlib.Path, default=None)
     args = ap.parse_args(argv)
-    lib = build(args.jobs, args.out)
-    print(lib)
+    with cf.ThreadPoolExecutor(max_workers=1) as ex:
+        ext = ex.submit(build_torch_ext, args.out)
+        lib = build(args.jobs, args.out)
+        print(lib)
+        print(ext.result())
     return 0
 
 

@@ -9,15 +9,22 @@ The torch-level helpers below take device tensors, check them, allocate the
 outputs and the fp32 row-statistic workspace with torch's caching allocator,
 and enqueue the kernels on torch's current stream for the tensors' device.
 Their `causal` argument is a bool (top-left when true) or the C ABI's code
-(0 none, 1 top-left, 2 bottom-right).
+(0 none, 1 top-left, 2 bottom-right). attention_fwd, attention_bwd and
+attention_bwdbwd hand the work to the torch extension _lib/_fhog_torch when
+it is built (the same checks, allocations and C-ABI call in C++, a few
+microseconds of host time instead of 9-20), bound to the entry points of the
+library loaded here; FLASH_HOG_TORCH_EXT=0 keeps them in Python.
 """
 
 from __future__ import annotations
 
 import ctypes
 import functools
+import importlib.machinery
+import importlib.util
 import os
 import pathlib
+import sysconfig
 
 import torch
 
@@ -74,6 +81,28 @@ def lib() -> ctypes.CDLL:
         fn.restype = res
         fn.argtypes = args
     return handle
+
+
+TORCH_EXT_ENV = "FLASH_HOG_TORCH_EXT"
+TORCH_EXT_PATH = LIB_PATH.parent / ("_fhog_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+@functools.cache
+def torch_ext():
+    """The _fhog_torch extension bound to lib()'s entry points, or None when it
+    is not built (or FLASH_HOG_TORCH_EXT=0): the Python wrappers then do the
+    same work."""
+    if os.environ.get(TORCH_EXT_ENV, "1") == "0" or not TORCH_EXT_PATH.exists():
+        return None
+    name = "flash_hog._lib._fhog_torch"
+    loader = importlib.machinery.ExtensionFileLoader(name, str(TORCH_EXT_PATH))
+    mod = importlib.util.module_from_spec(importlib.util.spec_from_loader(name, loader))
+    loader.exec_module(mod)
+    L = lib()
+    addr = lambda fn: ctypes.cast(fn, ctypes.c_void_p).value
+    mod.bind(addr(L.fhog_attention_fwd), addr(L.fhog_attention_bwd), addr(L.fhog_attention_bwdbwd),
+             addr(L.fhog_last_error), addr(L.fhog_status_string), FlashHogError)
+    return mod
 
 
 def check(status: int) -> None:
@@ -176,6 +205,9 @@ def attention_supported(batch: int, n_q: int, n_k: int, heads: int, kv_heads: in
 
 def attention_fwd(q, k, v, causal, scale: float):
     """O (B, T, N, H) in q's dtype and the natural-log logsumexp L (B, N, T) fp32."""
+    ext = torch_ext()
+    if ext is not None:
+        return ext.attention_fwd(q, k, v, causal_code(causal), float(scale))
     _check_inputs([("q", q), ("k", k), ("v", v)], q.dtype)
     B, Tq, Tk, N, Nk, Hd = _dims(q, k)
     _expect("v", v, k.shape)
@@ -191,6 +223,9 @@ def attention_fwd(q, k, v, causal, scale: float):
 
 def attention_bwd(q, k, v, o, dout, lse, causal, scale: float):
     """dQ, dK, dV of attention given its residual; also returns D (B, N, T) fp32."""
+    ext = torch_ext()
+    if ext is not None:
+        return ext.attention_bwd(q, k, v, o, dout, lse, causal_code(causal), float(scale))
     _check_inputs([("q", q), ("k", k), ("v", v), ("o", o), ("dout", dout)], q.dtype)
     _check_inputs([("q", q), ("lse", lse)])
     B, Tq, Tk, N, Nk, Hd = _dims(q, k)
@@ -212,6 +247,11 @@ def attention_bwd(q, k, v, o, dout, lse, causal, scale: float):
 def attention_bwdbwd(q, k, v, o, dout, ddq, ddk, ddv, lse, causal, scale: float,
                      return_stats: bool = False):
     """dQ2, dK2, dV2, ddO of the double backward [and the row statistics D, dD, B]."""
+    ext = torch_ext()
+    if ext is not None:
+        dq2, dk2, dv2, ddo, stats = ext.attention_bwdbwd(q, k, v, o, dout, ddq, ddk, ddv, lse, causal_code(causal),
+                                                         float(scale))
+        return (dq2, dk2, dv2, ddo, tuple(stats.unbind(0))) if return_stats else (dq2, dk2, dv2, ddo)
     _check_inputs([("q", q), ("k", k), ("v", v), ("o", o), ("dout", dout),
                    ("ddq", ddq), ("ddk", ddk), ("ddv", ddv)], q.dtype)
     _check_inputs([("q", q), ("lse", lse)])

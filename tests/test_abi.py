@@ -203,3 +203,46 @@ def test_supported_python_api_without_gpu():
     assert not ok and "dtype" in why
     with pytest.raises(ValueError, match="causal_alignment"):
         flash_hog.supported(**kw, causal_alignment="diagonal")
+
+
+def test_torch_extension_is_built_and_bound():
+    """The torch extension _fhog_torch (C++ calls of the C ABI) is built in-tree
+    and bound to the loaded library's entry points."""
+    from flash_hog import _hip
+
+    assert _hip.TORCH_EXT_PATH.exists(), f"{_hip.TORCH_EXT_PATH} missing: run python flash-hog_amd/build.py"
+    ext = _hip.torch_ext()
+    assert ext is not None
+    for name in ("attention_fwd", "attention_bwd", "attention_bwdbwd"):
+        assert callable(getattr(ext, name))
+
+
+def _python_path(monkeypatch):
+    from flash_hog import _hip
+
+    monkeypatch.setattr(_hip, "torch_ext", lambda: None)
+
+
+@pytest.mark.parametrize("which", ["fwd", "bwd", "bwdbwd"])
+def test_torch_extension_rejects_as_the_python_wrappers_do(which, monkeypatch):
+    """Host tensors are refused by the extension with the Python wrappers'
+    exception and message, and a non-tensor argument with a TypeError, before
+    anything reaches the GPU."""
+    import torch
+
+    from flash_hog import _hip
+
+    q = torch.zeros(1, 8, 2, 64, dtype=torch.bfloat16)
+    lse = torch.zeros(1, 2, 8)
+    args = {"fwd": (q, q, q), "bwd": (q, q, q, q, q, lse), "bwdbwd": (q, q, q, q, q, q, q, q, lse)}[which]
+    fn = getattr(_hip, "attention_" + which)
+
+    def outcome(*a):
+        with pytest.raises((ValueError, TypeError)) as e:
+            fn(*a, 1, 0.125)
+        return e.type, str(e.value)
+
+    got = outcome(*args)
+    assert outcome(args[0], 3, *args[2:])[0] is TypeError
+    _python_path(monkeypatch)
+    assert got == outcome(*args) == (ValueError, "q must be on a GPU device, got cpu")
