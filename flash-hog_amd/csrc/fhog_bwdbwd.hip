@@ -357,30 +357,13 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
   const int n = lane & 31, g = lane >> 5;
   const int nbh = p.batch * p.kv_heads;
   const int nkb = (p.nk + BKB - 1) / BKB;
-  // Key block `rank` of pair bh (causal: the longest key columns come first).
-  // With pairs = 1 the workgroup then also takes the mirror key block
-  // nkb - 1 - rank: causally block r sees the query tiles from r on, so a pair
-  // does about the same work for every r and the grid has no tail of short
-  // blocks.
-  //
-  // pairs = 2 is for a grid of exactly two workgroups per CU, nkb a multiple
-  // of 4. Workgroup i and i + (grid size) / 2 then share a CU, and i, placed
-  // first, is favoured by the wave arbiter (oldest first): with equal work it
-  // ends long before its neighbour, which then runs alone (measured at B4 N2048
-  // H16: 119 vs 144 us). So the favoured ranks j < q = nkb / 4 take the longer
-  // second block nkb - 1 - q - j and the others (j >= q) take
-  // nkb - 1 + q - j. With the work of block r proportional to nkb - r, the
-  // two workgroups of a CU then carry nkb + 1 + q and nkb + 1 - q units
-  // instead of nkb + 1 each (84 and 52 query tiles at nkb = 16; stage 2 at
-  // B4 N2048 H16 D64 went from 149.7 to 144.8 us).
+  // Key block `rank` of pair bh (causal: the longest key columns come first),
+  // and with pairs > 0 also a second one (block_pair).
   const GridSlot slot = grid_slot(blockIdx.x, nbh, pairs ? (nkb + 1) / 2 : nkb, chunk);
   const int bh = slot.pair;
-  const int first = slot.rank;
-  int second = nkb - 1 - slot.rank;
-  if (pairs == 2) second += slot.rank < nkb / 4 ? -(nkb / 4) : nkb / 4;
-  const int nblk = (pairs && second != first) ? 2 : 1;
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int kb = blk == 0 ? first : second;
+  const BlockPair bp = block_pair(slot.rank, nkb, pairs);
+  for (int blk = 0; blk < bp.count; ++blk) {
+    const int kb = blk == 0 ? bp.first : bp.second;
     if (blk > 0) __syncthreads();  // every wave is done with the previous block's ring
     const int b = bh / p.kv_heads, hk = bh % p.kv_heads;
     const int grp = p.heads / p.kv_heads;  // query heads per key/value head
@@ -672,11 +655,8 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stage
     // Pair causal key blocks when the grid outnumbers the resident workgroups.
     const int npairs = p.batch * p.kv_heads;
     const int resident = resident_workgroups(Occupancy<T, D>::value);
-    int pairs = CAUSAL && nkb * npairs > resident;
+    const int pairs = block_pairing(CAUSAL, nkb, npairs, resident, Occupancy<T, D>::value);
     const int nranks = pairs ? (nkb + 1) / 2 : nkb;
-    // One full round of two workgroups per CU (rank-major order, so ranks below
-    // nkb / 4 are the favoured first half of the grid): skewed pairs.
-    if (pairs && nkb % 4 == 0 && nranks * npairs == resident && Occupancy<T, D>::value == 2) pairs = 2;
     const int chunk = grid_chunk(npairs, nranks, resident);
     const dim3 grid(nranks * npairs);
     int e2;

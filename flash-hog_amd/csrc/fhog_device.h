@@ -454,6 +454,27 @@ __device__ __forceinline__ GridSlot grid_slot(int wg, int npairs, int nranks, in
   return GridSlot{rank, c * chunk + rem - rank * n};
 }
 
+// Mirror pairing of causal blocks. Block r of a causal grid holds work
+// proportional to nb - r (key-tiled) or r + 1 (query-tiled, in rank order:
+// rank r is block nb - 1 - r), so a workgroup that takes rank r and then rank
+// nb - 1 - r does about the same work for every r, and the grid has no tail of
+// short blocks. pairs = 2 is for a paired grid of exactly two workgroups per
+// CU (nb a multiple of 4): workgroup i and i + (grid size) / 2 then share a CU
+// and i, placed first, is favoured by the wave arbiter (oldest first), so with
+// equal work it ends long before its neighbour, which then runs alone. The
+// favoured ranks r < q = nb / 4 therefore take the longer second rank
+// nb - 1 - q - r and the others nb - 1 + q - r: the two workgroups of a CU then
+// carry nb + 1 + q and nb + 1 - q units of work. pairs = 0: one rank per
+// workgroup.
+struct BlockPair {
+  int first, second, count;
+};
+__device__ __forceinline__ BlockPair block_pair(int rank, int nb, int pairs) {
+  int second = nb - 1 - rank;
+  if (pairs == 2) second += rank < nb / 4 ? -(nb / 4) : nb / 4;
+  return BlockPair{rank, second, (pairs && second != rank) ? 2 : 1};
+}
+
 // Workgroups of 4 waves resident on the current device at once, at `waves`
 // waves per SIMD (0 if the device cannot be queried).
 inline int resident_workgroups(int waves) {
@@ -473,6 +494,16 @@ inline int grid_chunk(int npairs, int nranks, int resident) {
   if (resident <= 0 || (long)npairs * nranks <= 8L * resident) return npairs;
   const int c = resident / nranks / 8 * 8;
   return c < 8 ? 8 : (c < npairs ? c : npairs);
+}
+
+// The `pairs` argument of block_pair for a grid of nb causal blocks per
+// (batch, head) pair: mirror pairs when the unpaired grid outnumbers the
+// resident workgroups, skewed ones when the paired grid is exactly one round
+// at two workgroups per CU.
+inline int block_pairing(bool causal, int nb, int npairs, int resident, int waves) {
+  int pairs = causal && resident > 0 && (long)nb * npairs > resident;
+  if (pairs && nb % 4 == 0 && (long)((nb + 1) / 2) * npairs == resident && waves == 2) pairs = 2;
+  return pairs;
 }
 
 }  // namespace fhog
