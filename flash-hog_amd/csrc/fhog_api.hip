@@ -64,8 +64,6 @@ int check_shape(const Shape& s, const char* who) {
                 s.kv_heads);
   if (s.head_dim != 64 && s.head_dim != 128)
     return fail(FHOG_ERR_UNSUPPORTED, "%s: head_dim must be 64 or 128, got %d", who, s.head_dim);
-  if (s.dtype == FHOG_DTYPE_F32 && s.head_dim != 64)
-    return fail(FHOG_ERR_UNSUPPORTED, "%s: fp32 supports head_dim 64 only, got %d", who, s.head_dim);
   const long long rows = (long long)s.batch * s.heads * (s.n_q > s.n_k ? s.n_q : s.n_k);
   if (rows * s.head_dim >= (1ll << 40) || (long long)s.batch * s.heads * ((s.n_q > s.n_k ? s.n_q : s.n_k) + 31) / 32 >= (1ll << 31))
     return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: problem too large", who);
@@ -101,7 +99,8 @@ hipError_t dispatch(int dtype, int head_dim, bool causal, F&& f) {
     if (head_dim == 64) { FHOG_CASE(_Float16, 64) }
     FHOG_CASE(_Float16, 128)
   }
-  FHOG_CASE(float, 64)
+  if (head_dim == 64) { FHOG_CASE(float, 64) }
+  FHOG_CASE(float, 128)
 #undef FHOG_CASE
 }
 

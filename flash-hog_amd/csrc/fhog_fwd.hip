@@ -215,6 +215,8 @@ FHOG_INST(_Float16, 128, true)
 FHOG_INST(_Float16, 128, false)
 FHOG_INST(float, 64, true)
 FHOG_INST(float, 64, false)
+FHOG_INST(float, 128, true)
+FHOG_INST(float, 128, false)
 #undef FHOG_INST
 
 }  // namespace fhog

@@ -75,7 +75,7 @@ def _bwdbwd_args(ptr=16, batch=1, n_q=16, n_k=16, heads=1, kv_heads=1, head_dim=
     (dict(causal=3), 1, "causal must be 0 (none), 1 (top-left) or 2 (bottom-right)"),
     (dict(causal=-1), 1, "causal must be"),
     (dict(head_dim=96), 2, "head_dim must be 64 or 128"),
-    (dict(head_dim=128, dtype=0), 2, "fp32 supports head_dim 64"),
+    (dict(head_dim=96, dtype=0), 2, "head_dim must be 64 or 128"),
     (dict(scale=float("nan")), 1, "scale"),
     (dict(scale=float("inf")), 1, "scale must be finite"),
     (dict(scale=0.0), 2, "scale must be nonzero"),
@@ -166,8 +166,8 @@ def test_library_imports_no_allocating_hip_routine():
     (dict(head_dim=128, n_q=77, n_k=300, causal=2), 0, ""),
     (dict(dtype=0), 0, ""),
     (dict(heads=8, kv_heads=2, scale=-0.3), 0, ""),
+    (dict(head_dim=128, dtype=0), 0, ""),
     (dict(head_dim=96), 2, "head_dim must be 64 or 128"),
-    (dict(head_dim=128, dtype=0), 2, "fp32 supports head_dim 64"),
     (dict(heads=3, kv_heads=2), 1, "multiple of kv_heads"),
     (dict(scale=0.0), 2, "scale must be nonzero"),
     (dict(n_q=0), 1, "sizes must be >= 1"),

@@ -91,7 +91,8 @@ def test_padded_head_dims_keep_shapes():
 
     assert kernel_head_dim(torch.bfloat16, 96) == 128 and kernel_head_dim(torch.bfloat16, 1) == 64
     assert kernel_head_dim(torch.float16, 128) == 128 and kernel_head_dim(torch.bfloat16, 129) is None
-    assert kernel_head_dim(torch.float32, 48) == 64 and kernel_head_dim(torch.float32, 96) is None
+    assert kernel_head_dim(torch.float32, 48) == 64 and kernel_head_dim(torch.float32, 96) == 128
+    assert kernel_head_dim(torch.float32, 129) is None
     q = meta(2, 16, 4, 96).requires_grad_(True)
     k = meta(2, 16, 2, 96).requires_grad_(True)
     v = meta(2, 16, 2, 96).requires_grad_(True)

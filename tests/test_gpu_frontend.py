@@ -50,8 +50,8 @@ def test_backward_backward_single(is_causal, dtype, cuda_device):
 
 @pytest.mark.parametrize("head_dim,dtype,is_causal", [
     (32, torch.bfloat16, True), (80, torch.bfloat16, False), (96, torch.float16, True),
-    (16, torch.bfloat16, True), (40, torch.float32, True),
-], ids=["d32_bf16_causal", "d80_bf16", "d96_f16_causal", "d16_bf16_causal", "d40_f32_causal"])
+    (16, torch.bfloat16, True), (40, torch.float32, True), (96, torch.float32, False),
+], ids=["d32_bf16_causal", "d80_bf16", "d96_f16_causal", "d16_bf16_causal", "d40_f32_causal", "d96_f32"])
 def test_padded_head_dims(head_dim, dtype, is_causal, cuda_device):
     """Head dims the kernels do not take natively (the reference's kernel has no
     head-dim limit, flash_hog/jax/_pallas_gpu_kernel.py:80-101) run zero-padded
@@ -189,9 +189,10 @@ def test_vmap_hvp_equals_folded_batch(cuda_device):
           causal_alignment="bottom_right"), True),
     (dict(is_causal=True, seq_len=256, head_dim=96, num_q_heads=2, num_kv_heads=2), True),
     (dict(is_causal=True, seq_len=256, head_dim=160, num_q_heads=2, num_kv_heads=2), False),
-    (dict(is_causal=True, seq_len=256, head_dim=128, num_q_heads=2, num_kv_heads=2, dtype=torch.float32), False),
+    (dict(is_causal=True, seq_len=256, head_dim=128, num_q_heads=2, num_kv_heads=2, dtype=torch.float32), True),
+    (dict(is_causal=True, seq_len=256, head_dim=192, num_q_heads=2, num_kv_heads=2, dtype=torch.float32), False),
     (dict(is_causal=True, seq_len=256, head_dim=64, num_q_heads=3, num_kv_heads=2), False),
-], ids=["bench", "gqa_f16", "d128_br", "d96_padded", "d160", "f32_d128", "bad_groups"])
+], ids=["bench", "gqa_f16", "d128_br", "d96_padded", "d160", "f32_d128", "f32_d192", "bad_groups"])
 def test_supported_agrees_with_a_call(kw, expect, cuda_device):
     """flash_hog.supported (the reference's _tk_gpu.py:70-80 query) says True
     exactly where the front-end's double backward runs."""

@@ -34,7 +34,7 @@ def _problems(count=36, seed=2024):
     out = []
     for i in range(count):
         dtype = rnd.choice((BF16, BF16, F16, F32))
-        D = 64 if dtype == F32 else rnd.choice((64, 128))
+        D = rnd.choice((64, 128))
         H = rnd.choice((1, 2, 3, 4, 6, 8))
         Hk = rnd.choice([d for d in range(1, H + 1) if H % d == 0])
         B = rnd.choice((1, 2, 3))
