@@ -62,8 +62,10 @@ int check_shape(const Shape& s, const char* who) {
   if (s.heads % s.kv_heads != 0)
     return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: heads (%d) must be a multiple of kv_heads (%d)", who, s.heads,
                 s.kv_heads);
-  if (s.head_dim != 64 && s.head_dim != 128)
-    return fail(FHOG_ERR_UNSUPPORTED, "%s: head_dim must be 64 or 128, got %d", who, s.head_dim);
+  if (s.dtype == FHOG_DTYPE_F32 && s.head_dim != 64 && s.head_dim != 128)
+    return fail(FHOG_ERR_UNSUPPORTED, "%s: fp32 head_dim must be 64 or 128, got %d", who, s.head_dim);
+  if (s.head_dim != 64 && s.head_dim != 128 && s.head_dim != 256)
+    return fail(FHOG_ERR_UNSUPPORTED, "%s: head_dim must be 64, 128 or 256, got %d", who, s.head_dim);
   const long long rows = (long long)s.batch * s.heads * (s.n_q > s.n_k ? s.n_q : s.n_k);
   if (rows * s.head_dim >= (1ll << 40) || (long long)s.batch * s.heads * ((s.n_q > s.n_k ? s.n_q : s.n_k) + 31) / 32 >= (1ll << 31))
     return fail(FHOG_ERR_INVALID_ARGUMENT, "%s: problem too large", who);
@@ -93,11 +95,13 @@ hipError_t dispatch(int dtype, int head_dim, bool causal, F&& f) {
   return causal ? f.template operator()<T, D, true>() : f.template operator()<T, D, false>();
   if (dtype == FHOG_DTYPE_BF16) {
     if (head_dim == 64) { FHOG_CASE(__bf16, 64) }
-    FHOG_CASE(__bf16, 128)
+    if (head_dim == 128) { FHOG_CASE(__bf16, 128) }
+    FHOG_CASE(__bf16, 256)
   }
   if (dtype == FHOG_DTYPE_F16) {
     if (head_dim == 64) { FHOG_CASE(_Float16, 64) }
-    FHOG_CASE(_Float16, 128)
+    if (head_dim == 128) { FHOG_CASE(_Float16, 128) }
+    FHOG_CASE(_Float16, 256)
   }
   if (head_dim == 64) { FHOG_CASE(float, 64) }
   FHOG_CASE(float, 128)

@@ -182,13 +182,18 @@ bwd_q_kernel(BwdParams<T> p, int chunk) {
 // waves 2-3 those of each dO tile; wave 3 also loads the tile's L and D with
 // dword DMAs and, once they have landed, rewrites them in LDS as the initial
 // values of the S and dP accumulators (-L / scale and -D).
-template <typename T, int D, bool CAUSAL>
+//
+// At D = 256 the dK and dV accumulators of all 256 columns and the resident
+// K and V do not fit beside the score tiles in a wave's 512 registers, so the
+// launcher runs the kernel twice, for output column blocks [C0, C0 + DTO)
+// with C0 = 0 and 4 (each pass forms the full scores again).
+template <typename T, int D, bool CAUSAL, int C0>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
 bwd_k_kernel(BwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
-  constexpr int DT = D / 32;
+  constexpr int DTO = D > 128 ? D / 64 : D / 32;  // 32-column output blocks of this pass
   constexpr int BKB = 32 * kWaves;
   constexpr int BQ = 32;
   constexpr int NST = kStages;
@@ -229,9 +234,9 @@ bwd_k_kernel(BwdParams<T> p, int chunk) {
   const int qt_begin = CAUSAL ? max(0, kb * BKB - p.coff) / BQ : 0;
   const int total = nqt > qt_begin ? (nqt - qt_begin) * grp : 0;
 
-  f32x16 acc_dk[DT], acc_dv[DT];
+  f32x16 acc_dk[DTO], acc_dv[DTO];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) acc_dk[dt] = acc_dv[dt] = zero16();
+  for (int dt = 0; dt < DTO; ++dt) acc_dk[dt] = acc_dv[dt] = zero16();
 
   if (total > 0) {
     V8<T> kf[KS], vf[KS];
@@ -351,9 +356,9 @@ bwd_k_kernel(BwdParams<T> p, int chunk) {
           const V8<T> oP = cvt8<T>(s ? hi8(P) : lo8(P));
           const V8<T> oS = cvt8<T>(vdS);
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            acc_dv[dt] = mma<T>(fr.trf(sa, kTile, dt, s), oP, acc_dv[dt]);
-            acc_dk[dt] = mma<T>(fr.trf(sa, 0, dt, s), oS, acc_dk[dt]);
+          for (int dt = 0; dt < DTO; ++dt) {
+            acc_dv[dt] = mma<T>(fr.trf(sa, kTile, C0 + dt, s), oP, acc_dv[dt]);
+            acc_dk[dt] = mma<T>(fr.trf(sa, 0, C0 + dt, s), oS, acc_dk[dt]);
           }
         }
       }
@@ -364,10 +369,10 @@ bwd_k_kernel(BwdParams<T> p, int chunk) {
     T* dk = p.dk + kbase + (long)kj * rsk;
     T* dv = p.dv + kbase + (long)kj * rsk;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+    for (int dt = 0; dt < DTO; ++dt) {
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        const int d = 32 * dt + 8 * a + 4 * g;
+        const int d = 32 * (C0 + dt) + 8 * a + 4 * g;
         f32x4 x, y;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -393,8 +398,13 @@ hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t stream) {
                      grid_chunk(nq_pairs, nqb, resident));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL>), dim3(nkb * nk_pairs), dim3(kThreads), 0, stream, p,
+  hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL, 0>), dim3(nkb * nk_pairs), dim3(kThreads), 0, stream, p,
                      grid_chunk(nk_pairs, nkb, resident));
+  if constexpr (D > 128) {
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL, D / 64>), dim3(nkb * nk_pairs), dim3(kThreads), 0, stream, p,
+                       grid_chunk(nk_pairs, nkb, resident));
+  }
   return hipGetLastError();
 }
 
@@ -403,10 +413,14 @@ FHOG_INST(__bf16, 64, true)
 FHOG_INST(__bf16, 64, false)
 FHOG_INST(__bf16, 128, true)
 FHOG_INST(__bf16, 128, false)
+FHOG_INST(__bf16, 256, true)
+FHOG_INST(__bf16, 256, false)
 FHOG_INST(_Float16, 64, true)
 FHOG_INST(_Float16, 64, false)
 FHOG_INST(_Float16, 128, true)
 FHOG_INST(_Float16, 128, false)
+FHOG_INST(_Float16, 256, true)
+FHOG_INST(_Float16, 256, false)
 FHOG_INST(float, 64, true)
 FHOG_INST(float, 64, false)
 FHOG_INST(float, 128, true)

@@ -651,21 +651,24 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stage
     if (e != hipSuccess) return e;
   }
   if (stages & 2) {
-    if constexpr (sizeof(T) == 2 && D == 128) return launch_bwdbwd_stage2_k16<T, D, CAUSAL>(p, stream);
-    // Pair causal key blocks when the grid outnumbers the resident workgroups.
-    const int npairs = p.batch * p.kv_heads;
-    const int resident = resident_workgroups(Occupancy<T, D>::value);
-    const int pairs = block_pairing(CAUSAL, nkb, npairs, resident, Occupancy<T, D>::value);
-    const int nranks = pairs ? (nkb + 1) / 2 : nkb;
-    const int chunk = grid_chunk(npairs, nranks, resident);
-    const dim3 grid(nranks * npairs);
-    int e2;
-    if (std::is_same_v<T, __bf16> && std::frexp(p.scale, &e2) == 0.5f)  // scale = 2^(e2 - 1)
-      hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, std::is_same_v<T, __bf16>>), grid, dim3(kThreads), 0, stream, p,
-                         pairs, chunk);
-    else
-      hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, false>), grid, dim3(kThreads), 0, stream, p, pairs, chunk);
-    return hipGetLastError();
+    if constexpr (sizeof(T) == 2 && D >= 128) {
+      return launch_bwdbwd_stage2_k16<T, D, CAUSAL>(p, stream);
+    } else {
+      // Pair causal key blocks when the grid outnumbers the resident workgroups.
+      const int npairs = p.batch * p.kv_heads;
+      const int resident = resident_workgroups(Occupancy<T, D>::value);
+      const int pairs = block_pairing(CAUSAL, nkb, npairs, resident, Occupancy<T, D>::value);
+      const int nranks = pairs ? (nkb + 1) / 2 : nkb;
+      const int chunk = grid_chunk(npairs, nranks, resident);
+      const dim3 grid(nranks * npairs);
+      int e2;
+      if (std::is_same_v<T, __bf16> && std::frexp(p.scale, &e2) == 0.5f)  // scale = 2^(e2 - 1)
+        hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, std::is_same_v<T, __bf16>>), grid, dim3(kThreads), 0, stream,
+                           p, pairs, chunk);
+      else
+        hipLaunchKernelGGL((bwdbwd_k_kernel<T, D, CAUSAL, false>), grid, dim3(kThreads), 0, stream, p, pairs, chunk);
+      return hipGetLastError();
+    }
   }
   return hipSuccess;
 }
@@ -675,10 +678,14 @@ FHOG_INST(__bf16, 64, true)
 FHOG_INST(__bf16, 64, false)
 FHOG_INST(__bf16, 128, true)
 FHOG_INST(__bf16, 128, false)
+FHOG_INST(__bf16, 256, true)
+FHOG_INST(__bf16, 256, false)
 FHOG_INST(_Float16, 64, true)
 FHOG_INST(_Float16, 64, false)
 FHOG_INST(_Float16, 128, true)
 FHOG_INST(_Float16, 128, false)
+FHOG_INST(_Float16, 256, true)
+FHOG_INST(_Float16, 256, false)
 FHOG_INST(float, 64, true)
 FHOG_INST(float, 64, false)
 FHOG_INST(float, 128, true)

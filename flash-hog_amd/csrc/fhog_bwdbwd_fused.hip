@@ -1,5 +1,5 @@
 // Stage 1 of the Flash-HOG double backward (passes 1-3) in one sweep over the
-// keys, for 2-byte types at D = 64 and 128 (fhog_bwdbwd.hip holds the
+// keys, for 2-byte types at D = 64, 128 and 256 (fhog_bwdbwd.hip holds the
 // two-sweep stage 1 used for fp32, and stage 2). The math follows
 // flash_hog/_jax_refs/jax_impl.py:273-336 and the pass split of
 // flash_hog/jax/_pallas_gpu_kernel.py:149-278; outputs and row statistics are
@@ -69,7 +69,7 @@ struct Scores {
 
 template <typename T, int D, bool CAUSAL, bool PRE>
 __global__ void __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(2, 2)))
+__attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1, D <= 128 ? 2 : 1)))
 bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 32;       // 32-deep steps over the head dim (score products)
@@ -80,6 +80,8 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   // element-wise step of tile t) over a 4-stage ring (64 KiB); D = 128: the
   // accumulators and operands take twice the registers, so each tile's
   // scores are formed and finished in turn, over a 2-stage ring (64 KiB).
+  // D = 256: the same at one wave per SIMD (512 registers), over a 2-stage
+  // ring of 128 KiB (one workgroup per CU).
   constexpr bool PIPE = D == 64;
   constexpr int NST = PIPE ? 4 : 2;  // tiles t (finishing), t + 1 (scores), two in flight
   constexpr int kTile = G::kElems * (int)sizeof(T);
@@ -364,7 +366,7 @@ template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd_stage1_fused(const BwdBwdParams<T>& p, hipStream_t stream) {
   const int nqb = (p.nq + kQ * kWaves - 1) / (kQ * kWaves);
   const int npairs = p.batch * p.heads;
-  const int chunk = grid_chunk(npairs, nqb, resident_workgroups(2));
+  const int chunk = grid_chunk(npairs, nqb, resident_workgroups(D <= 128 ? 2 : 1));
   const dim3 grid(nqb * npairs);
   int e2;
   if (std::is_same_v<T, __bf16> && std::frexp(p.scale, &e2) == 0.5f)  // scale = 2^(e2 - 1)
@@ -385,6 +387,10 @@ FHOG_INST(__bf16, 128, true)
 FHOG_INST(__bf16, 128, false)
 FHOG_INST(_Float16, 128, true)
 FHOG_INST(_Float16, 128, false)
+FHOG_INST(__bf16, 256, true)
+FHOG_INST(__bf16, 256, false)
+FHOG_INST(_Float16, 256, true)
+FHOG_INST(_Float16, 256, false)
 #undef FHOG_INST
 
 }  // namespace fhog

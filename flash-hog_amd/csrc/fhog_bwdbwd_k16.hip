@@ -1,5 +1,5 @@
 // Stage 2 of the Flash-HOG double backward (pass 4: dK2, dV2) with 16 keys per
-// wave, for 2-byte types at D = 128. The math is that of fhog_bwdbwd.hip's
+// wave, for 2-byte types at D = 128 and 256. The math is that of fhog_bwdbwd.hip's
 // stage 2 (flash_hog/_jax_refs/jax_impl.py:273-336, the pass split of
 // flash_hog/jax/_pallas_gpu_kernel.py:309-391): per (query, key) pair, with
 // the per-query constants folded into the accumulator start values,
@@ -14,6 +14,8 @@
 // registers, two waves share each SIMD, and each query-side tile is read from
 // LDS by twice as many waves (the price: twice the LDS bytes per product).
 // At D = 64 the 32-key kernel already runs two waves per SIMD and is faster.
+// At D = 256 the state of 16 keys takes 446 registers: one wave per SIMD, one
+// workgroup per CU (the 32-key kernel spilled 1400 bytes per lane there).
 //
 // 16x16x32 layouts (fhog_device.h): score tiles are S = Q K^T (queries x
 // keys, two 16-query halves per 32-query tile); lane (n, g) holds key n and
@@ -46,7 +48,7 @@ struct Scores16 {
 
 template <typename T, int D, bool CAUSAL, bool PRE>
 __global__ void __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(2, 2)))
+__attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1, D <= 128 ? 2 : 1)))
 bwdbwd_k16_kernel(BwdBwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 32;             // 32-deep steps over the head dim (score products)
@@ -55,7 +57,8 @@ bwdbwd_k16_kernel(BwdBwdParams<T> p, int chunk) {
   constexpr int BQ = 32;                 // queries per streamed tile
   // Each iteration's scores are formed and then finished (the registers of a
   // second score set, for a software-pipelined loop, are not there at
-  // D = 128). Three stages of 24.5 KiB fit two workgroups per CU.
+  // D = 128). Three stages of 24.5 KiB fit two workgroups per CU at D = 128,
+  // three of 48.5 KiB one at D = 256.
   constexpr int NST = 3;
   constexpr int kTile = G::kElems * (int)sizeof(T);
   constexpr int kStat = 4 * BQ * (int)sizeof(float);
@@ -337,7 +340,7 @@ hipError_t launch_bwdbwd_stage2_k16(const BwdBwdParams<T>& p, hipStream_t stream
   static_assert(sizeof(T) == 2, "2-byte types only");
   const int nkb = (p.nk + kKeys * kWaves - 1) / (kKeys * kWaves);
   const int npairs = p.batch * p.kv_heads;
-  const int chunk = grid_chunk(npairs, nkb, resident_workgroups(2));
+  const int chunk = grid_chunk(npairs, nkb, resident_workgroups(D <= 128 ? 2 : 1));
   const dim3 grid(nkb * npairs);
   int e2;
   if (std::is_same_v<T, __bf16> && std::frexp(p.scale, &e2) == 0.5f)  // scale = 2^(e2 - 1)
@@ -353,6 +356,10 @@ FHOG_INST(__bf16, 128, true)
 FHOG_INST(__bf16, 128, false)
 FHOG_INST(_Float16, 128, true)
 FHOG_INST(_Float16, 128, false)
+FHOG_INST(__bf16, 256, true)
+FHOG_INST(__bf16, 256, false)
+FHOG_INST(_Float16, 256, true)
+FHOG_INST(_Float16, 256, false)
 #undef FHOG_INST
 
 }  // namespace fhog

@@ -209,10 +209,14 @@ FHOG_INST(__bf16, 64, true)
 FHOG_INST(__bf16, 64, false)
 FHOG_INST(__bf16, 128, true)
 FHOG_INST(__bf16, 128, false)
+FHOG_INST(__bf16, 256, true)
+FHOG_INST(__bf16, 256, false)
 FHOG_INST(_Float16, 64, true)
 FHOG_INST(_Float16, 64, false)
 FHOG_INST(_Float16, 128, true)
 FHOG_INST(_Float16, 128, false)
+FHOG_INST(_Float16, 256, true)
+FHOG_INST(_Float16, 256, false)
 FHOG_INST(float, 64, true)
 FHOG_INST(float, 64, false)
 FHOG_INST(float, 128, true)

@@ -62,7 +62,7 @@ template <typename T, int D, bool CAUSAL> hipError_t launch_bwd(const BwdParams<
 // stages: bit 0 = stage 1 (passes 1-3), bit 1 = stage 2 (pass 4).
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t s, int stages = 3);
-// Stage 1 in one sweep (2-byte types); launch_bwdbwd selects it.
+// Stage 1 in one sweep (2-byte types, D = 64 and 128); launch_bwdbwd selects it.
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd_stage1_fused(const BwdBwdParams<T>& p, hipStream_t s);
 // Stage 2 with 16 keys per wave (2-byte types, D = 128); launch_bwdbwd selects it.

@@ -34,7 +34,7 @@ from flash_hog.torch import _attention_impl as attn_impl
 # to any score, give zero output columns, and their gradients are dropped by the
 # padding's own backward, so the results are those of the unpadded problem (at
 # the cost of the copies and of the padded columns' arithmetic).
-_KERNEL_HEAD_DIMS = {torch.bfloat16: (64, 128), torch.float16: (64, 128), torch.float32: (64, 128)}
+_KERNEL_HEAD_DIMS = {torch.bfloat16: (64, 128, 256), torch.float16: (64, 128, 256), torch.float32: (64, 128)}
 
 
 def kernel_head_dim(dtype, head_dim: int) -> int | None:
@@ -61,9 +61,9 @@ def dot_product_attention(query, key, value, is_causal: bool = False, scale: flo
     flash_hog/_jax_refs/jax_impl.py:104-109); they agree when T == S.
 
     Like the reference's kernel, any head dim H >= 1 works up to the largest
-    one the kernels take (128 for bf16, fp16 and fp32); head dims the kernels
-    do not take natively (other than 64 and 128) are zero-padded to the next
-    one they do.
+    one the kernels take (256 for bf16 and fp16, 128 for fp32); head dims the
+    kernels do not take natively (other than 64, 128, 256) are zero-padded to
+    the next one they do.
     """
     if scale is None:
         scale = query.shape[-1] ** -0.5

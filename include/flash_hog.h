@@ -28,9 +28,10 @@
  * lse = +inf and zero gradients.
  * Tensor pointers must be 16-byte aligned, row-statistic pointers 4-byte aligned.
  *
- * Supported: dtype FHOG_DTYPE_{BF16,F16,F32} with head_dim 64 or 128; any
- * n_q, n_k >= 1 (ragged tails are masked); any finite nonzero scale,
- * negative included (scale 0 returns FHOG_ERR_UNSUPPORTED).
+ * Supported: dtype FHOG_DTYPE_{BF16,F16} with head_dim 64, 128 or 256,
+ * FHOG_DTYPE_F32 with head_dim 64 or 128; any n_q, n_k >= 1 (ragged tails
+ * are masked); any finite nonzero scale, negative included (scale 0 returns
+ * FHOG_ERR_UNSUPPORTED).
  */
 #ifndef FLASH_HOG_H_
 #define FLASH_HOG_H_

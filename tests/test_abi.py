@@ -74,8 +74,9 @@ def _bwdbwd_args(ptr=16, batch=1, n_q=16, n_k=16, heads=1, kv_heads=1, head_dim=
     (dict(heads=3, kv_heads=2), 1, "multiple of kv_heads"),
     (dict(causal=3), 1, "causal must be 0 (none), 1 (top-left) or 2 (bottom-right)"),
     (dict(causal=-1), 1, "causal must be"),
-    (dict(head_dim=96), 2, "head_dim must be 64 or 128"),
-    (dict(head_dim=96, dtype=0), 2, "head_dim must be 64 or 128"),
+    (dict(head_dim=96), 2, "head_dim must be 64, 128 or 256"),
+    (dict(head_dim=96, dtype=0), 2, "fp32 head_dim must be 64 or 128"),
+    (dict(head_dim=256, dtype=0), 2, "fp32 head_dim must be 64 or 128"),
     (dict(scale=float("nan")), 1, "scale"),
     (dict(scale=float("inf")), 1, "scale must be finite"),
     (dict(scale=0.0), 2, "scale must be nonzero"),
@@ -132,7 +133,7 @@ def _noalloc_args(ptr=16, batch=1, n_q=16, n_k=16, heads=1, kv_heads=1, head_dim
     (dict(ptr=None), 1, "q is null"),
     (dict(ptr=8), 1, "not 16-byte aligned"),
     (dict(scale=0.0), 2, "scale must be nonzero"),
-    (dict(head_dim=96), 2, "head_dim must be 64 or 128"),
+    (dict(head_dim=96), 2, "head_dim must be 64, 128 or 256"),
     # 1048577 (batch, head, query) rows: one more than the static scratch holds
     (dict(batch=1, heads=1, kv_heads=1, n_q=(1 << 20) + 1, n_k=64), 2, "exceeds the static scratch"),
     (dict(batch=64, heads=16, kv_heads=16, n_q=1025, n_k=1025), 2, "exceeds the static scratch"),
@@ -167,7 +168,9 @@ def test_library_imports_no_allocating_hip_routine():
     (dict(dtype=0), 0, ""),
     (dict(heads=8, kv_heads=2, scale=-0.3), 0, ""),
     (dict(head_dim=128, dtype=0), 0, ""),
-    (dict(head_dim=96), 2, "head_dim must be 64 or 128"),
+    (dict(head_dim=256, dtype=1, heads=4, kv_heads=2), 0, ""),
+    (dict(head_dim=96), 2, "head_dim must be 64, 128 or 256"),
+    (dict(head_dim=256, dtype=0), 2, "fp32 head_dim must be 64 or 128"),
     (dict(heads=3, kv_heads=2), 1, "multiple of kv_heads"),
     (dict(scale=0.0), 2, "scale must be nonzero"),
     (dict(n_q=0), 1, "sizes must be >= 1"),
@@ -198,7 +201,7 @@ def test_supported_python_api_without_gpu():
         assert flash_hog.supported(**kw) is False
     assert _hip.attention_supported(4, 2048, 2048, 16, 16, 64, torch.bfloat16, True, 0.125) == (True, "")
     ok, why = _hip.attention_supported(4, 2048, 2048, 16, 16, 96, torch.bfloat16, True, 0.125)
-    assert not ok and "head_dim must be 64 or 128" in why
+    assert not ok and "head_dim must be 64, 128 or 256" in why
     ok, why = _hip.attention_supported(4, 2048, 2048, 16, 16, 64, torch.float64, True, 0.125)
     assert not ok and "dtype" in why
     with pytest.raises(ValueError, match="causal_alignment"):

@@ -85,12 +85,13 @@ def test_unbatched_shapes():
 
 
 def test_padded_head_dims_keep_shapes():
-    """Head dims the kernels do not take natively are zero-padded to 64 or 128
+    """Head dims the kernels do not take natively are zero-padded to 64, 128 or 256
     and sliced back; the derivatives keep the caller's shapes."""
     from flash_hog.torch.attention import kernel_head_dim
 
     assert kernel_head_dim(torch.bfloat16, 96) == 128 and kernel_head_dim(torch.bfloat16, 1) == 64
-    assert kernel_head_dim(torch.float16, 128) == 128 and kernel_head_dim(torch.bfloat16, 129) is None
+    assert kernel_head_dim(torch.float16, 128) == 128 and kernel_head_dim(torch.bfloat16, 129) == 256
+    assert kernel_head_dim(torch.bfloat16, 257) is None and kernel_head_dim(torch.float16, 200) == 256
     assert kernel_head_dim(torch.float32, 48) == 64 and kernel_head_dim(torch.float32, 96) == 128
     assert kernel_head_dim(torch.float32, 129) is None
     q = meta(2, 16, 4, 96).requires_grad_(True)

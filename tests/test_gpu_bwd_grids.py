@@ -5,7 +5,7 @@ Both kernels of the first backward (dQ tiled over 128-query blocks, dK/dV over
 workgroup, with (batch, head) as the minor index (in chunks of pairs when the
 grid is longer than 8 rounds). These shapes give grids of one to several
 rounds, odd block counts, grouped heads, blocks that see nothing (top-left
-causal with N_K > N_Q, bottom-right with N_Q > N_K) and D = 128. Each shape is
+causal with N_K > N_Q, bottom-right with N_Q > N_K), D = 128 and D = 256. Each shape is
 checked on every (batch, head) against an fp32 closed form on the GPU (the
 first backward of tests/gpu_reference.py with a general causal mask), with
 the residual (O, L) from the fp32 forward. Tolerance: max|a - r| / max|r| <
@@ -42,6 +42,8 @@ SHAPES = [
     ("bottom_right", 16, 2600, 2304, 2, 2, 2, 64),
     # D = 128 (one wave per SIMD, 256 resident workgroups): two rounds
     ("d128", 16, 2048, 2048, 2, 2, 1, 128),
+    # D = 256: the dK/dV kernel runs twice, for the two halves of the output columns
+    ("d256_gqa2", 4, 1100, 1100, 4, 2, 1, 256),
 ]
 
 

@@ -50,12 +50,13 @@ def test_backward_backward_single(is_causal, dtype, cuda_device):
 
 @pytest.mark.parametrize("head_dim,dtype,is_causal", [
     (32, torch.bfloat16, True), (80, torch.bfloat16, False), (96, torch.float16, True),
-    (16, torch.bfloat16, True), (40, torch.float32, True), (96, torch.float32, False),
-], ids=["d32_bf16_causal", "d80_bf16", "d96_f16_causal", "d16_bf16_causal", "d40_f32_causal", "d96_f32"])
+    (16, torch.bfloat16, True), (40, torch.float32, True), (96, torch.float32, False), (160, torch.bfloat16, True),
+], ids=["d32_bf16_causal", "d80_bf16", "d96_f16_causal", "d16_bf16_causal", "d40_f32_causal", "d96_f32",
+        "d160_bf16_causal"])
 def test_padded_head_dims(head_dim, dtype, is_causal, cuda_device):
     """Head dims the kernels do not take natively (the reference's kernel has no
     head-dim limit, flash_hog/jax/_pallas_gpu_kernel.py:80-101) run zero-padded
-    to 64 or 128: forward, first and second derivatives against the fp64
+    to 64, 128 or 256: forward, first and second derivatives against the fp64
     autodiff oracle, at the unpadded head dim's default scale."""
     print("[case] frontend padded head dim", head_dim, dtype, is_causal, flush=True)
     x = make_inputs(2, 150, 150, 2, head_dim, dtype, seed=61)
@@ -188,11 +189,12 @@ def test_vmap_hvp_equals_folded_batch(cuda_device):
     (dict(is_causal=True, seq_len=200, head_dim=128, num_q_heads=4, num_kv_heads=4, kv_seq_len=300,
           causal_alignment="bottom_right"), True),
     (dict(is_causal=True, seq_len=256, head_dim=96, num_q_heads=2, num_kv_heads=2), True),
-    (dict(is_causal=True, seq_len=256, head_dim=160, num_q_heads=2, num_kv_heads=2), False),
+    (dict(is_causal=True, seq_len=256, head_dim=160, num_q_heads=2, num_kv_heads=2), True),
+    (dict(is_causal=True, seq_len=256, head_dim=320, num_q_heads=2, num_kv_heads=2), False),
     (dict(is_causal=True, seq_len=256, head_dim=128, num_q_heads=2, num_kv_heads=2, dtype=torch.float32), True),
     (dict(is_causal=True, seq_len=256, head_dim=192, num_q_heads=2, num_kv_heads=2, dtype=torch.float32), False),
     (dict(is_causal=True, seq_len=256, head_dim=64, num_q_heads=3, num_kv_heads=2), False),
-], ids=["bench", "gqa_f16", "d128_br", "d96_padded", "d160", "f32_d128", "f32_d192", "bad_groups"])
+], ids=["bench", "gqa_f16", "d128_br", "d96_padded", "d160_padded", "d320", "f32_d128", "f32_d192", "bad_groups"])
 def test_supported_agrees_with_a_call(kw, expect, cuda_device):
     """flash_hog.supported (the reference's _tk_gpu.py:70-80 query) says True
     exactly where the front-end's double backward runs."""

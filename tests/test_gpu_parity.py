@@ -47,6 +47,10 @@ CASES = [
     ("f32_bottom_right_gqa", 2, 64, 150, 4, 2, 64, F32, BR, 1.0),
     ("f16_bottom_right_mqa_d128", 1, 130, 257, 2, 1, 128, F16, BR, 1.0),
     ("bf16_bottom_right_square", 1, 256, 256, 2, 2, 64, BF16, BR, 1.0),
+    # D = 256 (2-byte types)
+    ("bf16_d256_causal", 1, 200, 200, 2, 2, 256, BF16, TL, 1.0),
+    ("f16_d256_gqa2_ragged_noncausal", 2, 77, 130, 4, 2, 256, F16, NONE, 0.5),
+    ("bf16_d256_bottom_right_long_q", 1, 150, 90, 2, 1, 256, BF16, BR, 1.0),
     # fp32 at D = 128
     ("f32_d128_causal", 1, 160, 160, 2, 2, 128, F32, TL, 1.0),
     ("f32_d128_gqa2_ragged_noncausal", 2, 77, 130, 4, 2, 128, F32, NONE, 1.0),
@@ -71,6 +75,8 @@ SCALE_CASES = [
     ("bf16_d128_noncausal_ragged_scale_0.0625", 2, 150, 230, 2, 2, 128, BF16, NONE, 0.0625),
     ("f32_causal_scale_-0.125", 1, 96, 96, 2, 2, 64, F32, TL, -0.125),
     ("f32_d128_causal_scale_0.3", 1, 100, 100, 2, 2, 128, F32, TL, 0.3),
+    ("bf16_d256_causal_scale_0.0625", 1, 100, 100, 2, 2, 256, BF16, TL, 0.0625),
+    ("bf16_d256_noncausal_scale_-0.05", 1, 100, 120, 2, 2, 256, BF16, NONE, -0.05),
 ]
 SCALE_IDS = [c[0] for c in SCALE_CASES]
 

@@ -1,8 +1,8 @@
 """The double backward on shapes that select each of stage 2's grid layouts.
 
-Stage 2 (pass 4, tiled over key blocks: 128 keys at D = 64, 64 keys in the
-16-key-per-wave kernel used for 2-byte types at D = 128, which keeps plain
-rank-major or chunked order) lays its grid out by the problem's
+Stage 2 (pass 4, tiled over key blocks: 128 keys at D = 64 and 256, 64 keys
+in the 16-key-per-wave kernel used for 2-byte types at D = 128, which keeps
+plain rank-major or chunked order) lays its grid out by the problem's
 size: one key block per workgroup when the grid fits on the GPU at once; for
 larger causal grids a workgroup takes key block r and then its mirror
 nkb - 1 - r (odd nkb leaves the middle block alone); and when that paired grid
@@ -52,6 +52,9 @@ SHAPES = [
     ("d128_empty_blocks", 16, 1024, 2304, 2, 2, 1, 128),
     # 16 blocks x 288 pairs = 9 rounds of 512 workgroups: chunked grid order
     ("d128_chunked", 144, 1024, 1024, 2, 2, 1, 128),
+    # D = 256 (the 32-key kernel at one wave per SIMD, 256 resident workgroups):
+    # 18 key blocks x 32 pairs, mirror pairs without the skew
+    ("d256_mirror_pairs", 16, 2304, 2304, 2, 2, 1, 256),
 ]
 
 

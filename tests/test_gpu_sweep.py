@@ -4,8 +4,9 @@ fp64 oracle.
 The hand-picked cases of test_gpu_parity.py cover each feature on its own;
 this sweep mixes them: batch 1-3, query and key lengths 1-300 drawn
 independently (ragged tails, N_Q != N_K, single tokens), 1-8 query heads with
-a random divisor as key/value heads (MHA, GQA, MQA), head dim 64 or 128,
-bf16 / fp16 / fp32, no mask / top-left / bottom-right causal (rows without
+a random divisor as key/value heads (MHA, GQA, MQA), head dim 64, 128 or 256
+(64 or 128 in fp32), bf16 / fp16 / fp32, no mask / top-left / bottom-right
+causal (rows without
 keys included), and the default or a random softmax scale, negative ones
 included. Each problem runs the forward, the first backward and the double
 backward through the C ABI; O, L, dQ, dK, dV, D, dQ2, dK2, dV2, ddO and the row
@@ -34,7 +35,7 @@ def _problems(count=36, seed=2024):
     out = []
     for i in range(count):
         dtype = rnd.choice((BF16, BF16, F16, F32))
-        D = rnd.choice((64, 128))
+        D = rnd.choice((64, 128) if dtype == F32 else (64, 128, 256))
         H = rnd.choice((1, 2, 3, 4, 6, 8))
         Hk = rnd.choice([d for d in range(1, H + 1) if H % d == 0])
         B = rnd.choice((1, 2, 3))
