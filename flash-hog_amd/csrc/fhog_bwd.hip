@@ -32,10 +32,15 @@ constexpr int kStages = 4;  // 3 stages: 2.6 % slower at B4 N2048 H16
 template <typename T, int D> struct Occupancy {
   static constexpr int value = (sizeof(T) == 2 && D == 64) ? 2 : 1;
 };
+// The dQ kernel fits two waves per SIMD at D = 128 too (238 VGPRs, no spill;
+// first backward at B4 N2048 H16 causal 495 against 430 us).
+template <typename T, int D> struct OccupancyQ {
+  static constexpr int value = (sizeof(T) == 2 && D <= 128) ? 2 : 1;
+};
 
 template <typename T, int D, bool CAUSAL>
 __global__ void __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
+__attribute__((amdgpu_waves_per_eu(OccupancyQ<T, D>::value, OccupancyQ<T, D>::value)))
 bwd_q_kernel(BwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
@@ -395,7 +400,7 @@ hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t stream) {
   const int resident = resident_workgroups(Occupancy<T, D>::value);
   const int nq_pairs = p.batch * p.heads, nk_pairs = p.batch * p.kv_heads;
   hipLaunchKernelGGL((bwd_q_kernel<T, D, CAUSAL>), dim3(nqb * nq_pairs), dim3(kThreads), 0, stream, p,
-                     grid_chunk(nq_pairs, nqb, resident));
+                     grid_chunk(nq_pairs, nqb, resident_workgroups(OccupancyQ<T, D>::value)));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL, 0>), dim3(nkb * nk_pairs), dim3(kThreads), 0, stream, p,
