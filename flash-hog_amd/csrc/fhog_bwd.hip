@@ -28,19 +28,25 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kStages = 4;  // 3 stages: 2.6 % slower at B4 N2048 H16
 
 // Waves per SIMD the register allocator is asked to allow: two for 2-byte
-// types at D = 64, one otherwise.
+// types at D = 64 and 128 (at D = 128 the dQ kernel takes 238 VGPRs and the
+// dK/dV kernel, in two column passes, 242; first backward at B4 N2048 H16
+// causal 495 -> 403-417 us), one otherwise.
 template <typename T, int D> struct Occupancy {
-  static constexpr int value = (sizeof(T) == 2 && D == 64) ? 2 : 1;
-};
-// The dQ kernel fits two waves per SIMD at D = 128 too (238 VGPRs, no spill;
-// first backward at B4 N2048 H16 causal 495 against 430 us).
-template <typename T, int D> struct OccupancyQ {
   static constexpr int value = (sizeof(T) == 2 && D <= 128) ? 2 : 1;
 };
+// Whether the dK/dV kernel runs as two passes over halves of the output
+// columns (each forming the full scores): at D = 256 all columns'
+// accumulators beside the resident K and V spilled 740 bytes per lane; for
+// 2-byte types at D = 128 they took 401 registers (one wave per SIMD) against
+// 242 per pass (two waves).
+template <typename T, int D> struct KSplit {
+  static constexpr bool value = D > 128 || (sizeof(T) == 2 && D == 128);
+};
+
 
 template <typename T, int D, bool CAUSAL>
 __global__ void __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(OccupancyQ<T, D>::value, OccupancyQ<T, D>::value)))
+__attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
 bwd_q_kernel(BwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
@@ -188,17 +194,17 @@ bwd_q_kernel(BwdParams<T> p, int chunk) {
 // dword DMAs and, once they have landed, rewrites them in LDS as the initial
 // values of the S and dP accumulators (-L / scale and -D).
 //
-// At D = 256 the dK and dV accumulators of all 256 columns and the resident
-// K and V do not fit beside the score tiles in a wave's 512 registers, so the
-// launcher runs the kernel twice, for output column blocks [C0, C0 + DTO)
-// with C0 = 0 and 4 (each pass forms the full scores again).
+// With KSplit (2-byte types at D = 128 and 256) the launcher runs the kernel
+// twice, for output column blocks [C0, C0 + DTO) with C0 = 0 and D / 64, each
+// pass forming the full scores again, so that the dK and dV accumulators of
+// half the columns fit beside the resident K and V.
 template <typename T, int D, bool CAUSAL, int C0>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(Occupancy<T, D>::value, Occupancy<T, D>::value)))
 bwd_k_kernel(BwdParams<T> p, int chunk) {
   typedef SwzTile<T, D> G;
   constexpr int KS = D / 16;
-  constexpr int DTO = D > 128 ? D / 64 : D / 32;  // 32-column output blocks of this pass
+  constexpr int DTO = KSplit<T, D>::value ? D / 64 : D / 32;  // 32-column output blocks of this pass
   constexpr int BKB = 32 * kWaves;
   constexpr int BQ = 32;
   constexpr int NST = kStages;
@@ -400,12 +406,12 @@ hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t stream) {
   const int resident = resident_workgroups(Occupancy<T, D>::value);
   const int nq_pairs = p.batch * p.heads, nk_pairs = p.batch * p.kv_heads;
   hipLaunchKernelGGL((bwd_q_kernel<T, D, CAUSAL>), dim3(nqb * nq_pairs), dim3(kThreads), 0, stream, p,
-                     grid_chunk(nq_pairs, nqb, resident_workgroups(OccupancyQ<T, D>::value)));
+                     grid_chunk(nq_pairs, nqb, resident));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL, 0>), dim3(nkb * nk_pairs), dim3(kThreads), 0, stream, p,
                      grid_chunk(nk_pairs, nkb, resident));
-  if constexpr (D > 128) {
+  if constexpr (KSplit<T, D>::value) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL, D / 64>), dim3(nkb * nk_pairs), dim3(kThreads), 0, stream, p,
                        grid_chunk(nk_pairs, nkb, resident));
