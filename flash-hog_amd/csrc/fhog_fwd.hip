@@ -26,9 +26,10 @@ constexpr int kStages = 4;  // 3 stages: 0.5-1 % slower
 // Waves per SIMD the register allocator is asked to allow: three for 2-byte
 // types at D = 64 (119 VGPRs; 50.7 against 55.4 us at two waves, B4 N2048 H16
 // causal, and four waves are no faster), two at D = 128 (190 VGPRs, no spill;
-// 147.7 against 86.3 us at one wave, B4 N2048 H16 causal), one otherwise.
+// 147.7 against 86.3 us at one wave, B4 N2048 H16 causal) and for fp32 at
+// D = 64 (154 VGPRs; 167 against 154 us at B2 N2048 H8), one otherwise.
 template <typename T, int D> struct Occupancy {
-  static constexpr int value = sizeof(T) != 2 ? 1 : D == 64 ? 3 : D == 128 ? 2 : 1;
+  static constexpr int value = sizeof(T) != 2 ? (D == 64 ? 2 : 1) : D == 64 ? 3 : D == 128 ? 2 : 1;
 };
 
 template <typename T, int D, bool CAUSAL>
