@@ -126,24 +126,43 @@ def _no_derivative(name):
     return staticmethod(backward)
 
 
-def _kernel_function(name, op, n_tensors):
-    def forward(*args):
-        return op(*args)
-
-    def setup_context(ctx, inputs, output):
-        ctx.mark_non_differentiable(*output)
-
-    return type(name, (torch.autograd.Function,), {
-        "generate_vmap_rule": True,
-        "forward": staticmethod(forward),
-        "setup_context": staticmethod(setup_context),
-        "backward": _no_derivative(name),
-    })
+def _mark_outputs(ctx, inputs, output):
+    ctx.mark_non_differentiable(*output)
 
 
-_FwdKernel = _kernel_function("flash_hog_attention_fwd", attention_fwd_op, 3)
-_BwdKernel = _kernel_function("flash_hog_attention_bwd", attention_bwd_op, 6)
-_BwdBwdKernel = _kernel_function("flash_hog_attention_bwdbwd", attention_bwdbwd_op, 9)
+# forward spells out its parameters: torch.compile reads a forward whose first
+# parameter is variadic as one that takes ctx.
+class _FwdKernel(torch.autograd.Function):
+    generate_vmap_rule = True
+
+    @staticmethod
+    def forward(q, k, v, causal, scale):
+        return attention_fwd_op(q, k, v, causal, scale)
+
+    setup_context = staticmethod(_mark_outputs)
+    backward = _no_derivative("flash_hog_attention_fwd")
+
+
+class _BwdKernel(torch.autograd.Function):
+    generate_vmap_rule = True
+
+    @staticmethod
+    def forward(q, k, v, o, dout, lse, causal, scale):
+        return attention_bwd_op(q, k, v, o, dout, lse, causal, scale)
+
+    setup_context = staticmethod(_mark_outputs)
+    backward = _no_derivative("flash_hog_attention_bwd")
+
+
+class _BwdBwdKernel(torch.autograd.Function):
+    generate_vmap_rule = True
+
+    @staticmethod
+    def forward(q, k, v, o, dout, ddq, ddk, ddv, lse, causal, scale):
+        return attention_bwdbwd_op(q, k, v, o, dout, ddq, ddk, ddv, lse, causal, scale)
+
+    setup_context = staticmethod(_mark_outputs)
+    backward = _no_derivative("flash_hog_attention_bwdbwd")
 
 
 # ---------------------------------------------------------------- wrappers

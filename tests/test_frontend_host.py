@@ -104,3 +104,21 @@ def test_padded_head_dims_keep_shapes():
     assert [t.shape for t in h] == [q.shape, k.shape, v.shape]
     out = torch.func.vmap(attn)(meta(3, 2, 16, 4, 40), meta(3, 2, 16, 4, 40), meta(3, 2, 16, 4, 40))
     assert out.shape == (3, 2, 16, 4, 40)
+
+
+def test_torch_compile_traces_forward_and_gradient():
+    """torch.compile (aot_eager backend, whole graph, no graph break) traces
+    the forward and its gradient through the kernel operators' fake
+    implementations. A second derivative of a compiled graph is refused by
+    torch itself (aot_autograd graphs are once differentiable); eager
+    grad-of-grad is what the GPU tests cover."""
+    q, k, v = meta(2, 64, 4, 64), meta(2, 64, 2, 64), meta(2, 64, 2, 64)
+    out = torch.compile(attn, backend="aot_eager", fullgraph=True)(q, k, v)
+    assert out.shape == q.shape
+
+    def loss(q, k, v):
+        return attn(q, k, v, causal_alignment="bottom_right").float().sum()
+
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    g = torch.autograd.grad(torch.compile(loss, backend="aot_eager", fullgraph=True)(qr, kr, vr), (qr, kr, vr))
+    assert [t.shape for t in g] == [q.shape, k.shape, v.shape]

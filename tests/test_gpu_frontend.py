@@ -214,3 +214,25 @@ def test_supported_agrees_with_a_call(kw, expect, cuda_device):
     else:
         with pytest.raises((ValueError, RuntimeError)):
             fhog_bwd_bwd(q, k, v, do, ddq, ddk, ddv, kw["is_causal"], None, causal_alignment=align)
+
+
+def test_torch_compile_matches_eager(cuda_device):
+    """A torch.compile'd (aot_eager backend, whole graph) forward and gradient
+    run the same kernels as eager: outputs and gradients bitwise equal."""
+    import flash_hog
+
+    print("[case] frontend torch.compile", flush=True)
+    x = {n: t.to(cuda_device) for n, t in make_inputs(2, 192, 192, 4, 64, torch.bfloat16, seed=21, kv_heads=2).items()}
+
+    def loss(q, k, v):
+        out = flash_hog.dot_product_attention(q, k, v, is_causal=True)
+        return (out.float() * x["do"].float()).sum(), out
+
+    results = []
+    for fn in (loss, torch.compile(loss, backend="aot_eager", fullgraph=True)):
+        q, k, v = (x[n].clone().requires_grad_(True) for n in ("q", "k", "v"))
+        val, out = fn(q, k, v)
+        results.append((out.detach(), *torch.autograd.grad(val, (q, k, v))))
+    torch.cuda.synchronize()
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
