@@ -6,8 +6,8 @@ PyTorch front-end with the same signature; both call the same HIP kernels
 through the C ABI in include/flash_hog.h.
 """
 
-from flash_hog._types import MaskType
+from flash_hog._types import MaskType, TuningConfig
 from flash_hog.torch._hip_gpu import supported
 from flash_hog.torch.attention import dot_product_attention
 
-__all__ = ["MaskType", "dot_product_attention", "supported"]
+__all__ = ["MaskType", "TuningConfig", "dot_product_attention", "supported"]

@@ -11,6 +11,7 @@ of the reference's jax_refs (flash_hog/_jax_refs/jax_impl.py:104-109); it is
 an addition of this package, valued outside the range of JAX's members.
 """
 
+import dataclasses
 import enum
 
 # Values of the C ABI's `causal` argument (include/flash_hog.h, enum fhog_causal).
@@ -48,3 +49,23 @@ def causal_code(mask_type: MaskType) -> int:
 def is_causal(mask_type: MaskType) -> bool:
     """True for the causal mask types (either alignment)."""
     return causal_code(mask_type) != CAUSAL_NONE
+
+
+@dataclasses.dataclass(frozen=True)
+class TuningConfig:
+    """The reference's tile configuration of its Pallas kernel (same fields
+    and defaults, flash_hog/jax/_pallas_gpu_kernel.py:22-29), accepted by
+    flash_bwdbwd so that calls written for the reference run unchanged.
+
+    The HIP kernels' tiles are compile-time constants chosen per dtype and
+    head dim on MI355X (128 rows per workgroup, 32-row streamed tiles, 16 or
+    32 rows per wave), and any sequence length works, so a TuningConfig does
+    not change the kernels or their results; in the reference too it only
+    changes speed (and requires sequence lengths divisible by its tiles,
+    :84-86, which these kernels do not)."""
+    tile_q: int
+    tile_k: int
+    max_concurrent_steps: int
+    epilogue_tile_n: int = 64
+    grid_minor_dim: int = 0
+    grid_tile_width: int = 1

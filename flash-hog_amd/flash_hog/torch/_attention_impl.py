@@ -18,8 +18,12 @@ public rules pass around (flash_hog/jax/attention.py:71).
 
 from __future__ import annotations
 
-from flash_hog._types import MaskType
+from flash_hog._types import MaskType, TuningConfig
 from flash_hog.torch import _hip_gpu
+
+
+# The configuration the reference's rule passes (_attention_impl.py:297).
+_CONFIG = TuningConfig(tile_q=32, tile_k=32, max_concurrent_steps=4)
 
 
 def dot_product_attention_fwd(query, key, value, mask_type: MaskType, scale: float):
@@ -51,6 +55,6 @@ def dot_product_attention_bwd_rule_bwd_rule(mask_type: MaskType, scale: float, r
     ddQ, ddK, ddV = g
     dQ2, dK2, dV2, ddO = _hip_gpu.flash_bwdbwd(
         Q=query, K=key, V=value, O=out, dO=dO, ddQ=ddQ, ddK=ddK, ddV=ddV, L=activation,
-        mask_type=mask_type, scale=scale)
+        mask_type=mask_type, scale=scale, config=_CONFIG)
     d_res = (dQ2, dK2, dV2, None, None)
     return d_res, ddO

@@ -22,7 +22,7 @@ from __future__ import annotations
 import torch
 
 from flash_hog import _hip
-from flash_hog._types import MaskType, causal_code
+from flash_hog._types import MaskType, TuningConfig, causal_code
 
 
 def _default_scale(x, scale):
@@ -202,8 +202,13 @@ def flash_bwd(query, key, value, out, dO, activation, *, mask_type: MaskType, sc
                             _default_scale(query, scale))
 
 
-def flash_bwdbwd(Q, K, V, O, dO, ddQ, ddK, ddV, L, *, mask_type: MaskType, scale: float | None):
-    """Returns (dQ2, dK2, dV2, ddO) (flash_hog/jax/_pallas_gpu.py:51-114)."""
+def flash_bwdbwd(Q, K, V, O, dO, ddQ, ddK, ddV, L, *, mask_type: MaskType, scale: float | None,
+                 config: TuningConfig | None = None):
+    """Returns (dQ2, dK2, dV2, ddO) (flash_hog/jax/_pallas_gpu.py:51-114).
+    config is the reference's tile configuration, accepted and type-checked
+    for call compatibility; the HIP kernels' tiles are fixed (TuningConfig)."""
+    if config is not None and not isinstance(config, TuningConfig):
+        raise TypeError(f"config must be a flash_hog TuningConfig, got {type(config).__name__}")
     if Q.ndim == 3:
         res = flash_bwdbwd(*_batchify(Q, K, V, O, dO, ddQ, ddK, ddV, L), mask_type=mask_type, scale=scale)
         return tuple(r[0] for r in res)

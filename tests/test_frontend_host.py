@@ -122,3 +122,19 @@ def test_torch_compile_traces_forward_and_gradient():
     qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
     g = torch.autograd.grad(torch.compile(loss, backend="aot_eager", fullgraph=True)(qr, kr, vr), (qr, kr, vr))
     assert [t.shape for t in g] == [q.shape, k.shape, v.shape]
+
+
+def test_flash_bwdbwd_takes_the_reference_tuning_config():
+    """flash_bwdbwd accepts the reference's TuningConfig (same fields and
+    defaults, _pallas_gpu_kernel.py:22-29) and rejects anything else as config."""
+    from flash_hog import TuningConfig
+    from flash_hog.torch import _hip_gpu
+
+    cfg = TuningConfig(tile_q=32, tile_k=32, max_concurrent_steps=4)
+    assert (cfg.epilogue_tile_n, cfg.grid_minor_dim, cfg.grid_tile_width) == (64, 0, 1)
+    q, k = meta(1, 64, 2, 64), meta(1, 64, 2, 64)
+    lse = meta(1, 2, 64, dtype=torch.float32)
+    outs = _hip_gpu.flash_bwdbwd(q, k, k, q, q, q, k, k, lse, mask_type=MaskType.CAUSAL, scale=None, config=cfg)
+    assert [t.shape for t in outs] == [q.shape, k.shape, k.shape, q.shape]
+    with pytest.raises(TypeError, match="TuningConfig"):
+        _hip_gpu.flash_bwdbwd(q, k, k, q, q, q, k, k, lse, mask_type=MaskType.CAUSAL, scale=None, config={"tile_q": 32})
