@@ -21,13 +21,22 @@
 // sum P u K, sum P K, ddO part). The dP accumulator starts at -D, so it ends
 // as u.
 //
+// Rounding. The ddO accumulator takes x rounded to T (bf16 or fp16) as the
+// operand of sum_j x V, and sum_j x V - dD O cancels to the small
+// sum_j x (V_j - O) when a row's keys carry similar P ddS. So the epilogue
+// subtracts dD' O with dD' = sum_j T(x_j), the dD of the rounded values (four
+// v_dot2 with ones per 32-key tile), and the cancellation leaves no rounding
+// residue of x; dD itself, B and dQ2 keep the unrounded sum. Against a CPU
+// model of this kernel's roundings over 40 random bf16 problems, this halves
+// the worst relative error of ddO, dQ2 and dK2 (0.020 -> 0.009 where rows see
+// few keys, as with N_K = 34 under a causal mask).
+//
 // Rows that see exactly one key (the first row of a causal problem, or every
 // row when N_K = 1). There P = 1, dS = dS2 = ddP = 0, so dQ2 = 0 and ddO =
-// ddV_0 exactly, while the sums above cancel only up to the bf16 rounding of
-// X and x (about 1e-2 at unit-size inputs where the exact value is 0). The
-// epilogue writes dQ2 = 0 for such rows and subtracts bf16(dD) O instead of
-// dD O from the ddO accumulator: with one key, x = dD and O = V_0, so that
-// cancels the rounding of x exactly, and c = <dO, ddO> and B follow exactly.
+// ddV_0 exactly. With one key x = dD' and O = V_0, so ddO comes out exact;
+// dQ2's sums cancel only up to the rounding of X and x (about 1e-2 at
+// unit-size inputs where the exact value is 0), and the epilogue writes
+// dQ2 = 0 for such rows.
 //
 // Sixteen queries per wave. The five accumulators of 32 queries would not fit
 // beside the score tiles in the 256 registers of a wave that shares its SIMD
@@ -190,7 +199,8 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   f32x4 acc_a[DB], acc_s[DB], acc_p[DB], acc_o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc_a[db] = acc_s[db] = acc_p[db] = acc_o[db] = zero4();
-  float dd_acc = 0.f;
+  float dd_acc = 0.f;  // dD = sum P ddS over this lane's keys
+  float ddr_acc = 0.f;  // the same sum over P ddS rounded to T, as the ddO products take it
   const f32x4 init_u = {nD, nD, nD, nD};
 
   // Score tiles of the key tile in slot sa (K at 0, V at kTile, ddK at
@@ -232,6 +242,7 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
       vX[e] = fmaf(x, u, P * sc.dPa[kb][i]);      // P (dPa + ddS u)
     }
     const V8<T> oP = cvt8<T>(vP), ox = cvt8<T>(vx), ou = cvt8<T>(vu), oX = cvt8<T>(vX);
+    ddr_acc = add_sum8<T>(ox, ddr_acc);
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
       const V8<T> tK = fr.trf(sa, 0, db);
@@ -312,9 +323,11 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   }
 
   const float dD = group4_sum(dd_acc);
+  // ddO = acc_o - dD O, with dD summed over the T-rounded x that acc_o took
+  // (see above).
+  const float dDo = group4_sum(ddr_acc);
   // A row that sees exactly one key (see above).
   const bool one_key = (CAUSAL ? min(p.nk, qi + p.coff + 1) : p.nk) == 1;
-  const float dDo = one_key ? (float)(T)dD : dD;  // the dD that multiplies O in ddO
   // ddO = acc_o - dD O and c = <dO, ddO>, from this lane's four columns of
   // each 16-column block (16 db + 4 g + i), summed over the four lane groups.
   const long roff = qbase + (long)qi * rs;

@@ -17,6 +17,8 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 #include <stdint.h>
 
 namespace fhog {
@@ -393,6 +395,23 @@ template <> __device__ __forceinline__ f32x4 mma16<_Float16>(f16x8 a, f16x8 b, f
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
 // Sum over the four 16-lane groups (the lanes that hold the same column n).
+// acc + the sum of the eight values of v as rounded to T (the values an MFMA
+// that takes v as an operand multiplies), by dot products with ones.
+template <typename T> __device__ __forceinline__ float add_sum8(V8<T> v, float acc) {
+  typedef T T2 __attribute__((ext_vector_type(2)));
+  const T2 ones = {(T)1.0f, (T)1.0f};
+  const T2 pairs[4] = {__builtin_shufflevector(v, v, 0, 1), __builtin_shufflevector(v, v, 2, 3),
+                       __builtin_shufflevector(v, v, 4, 5), __builtin_shufflevector(v, v, 6, 7)};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (std::is_same_v<T, __bf16>)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(pairs[i], ones, acc, false);
+    else
+      acc = __builtin_amdgcn_fdot2(pairs[i], ones, acc, false);
+  }
+  return acc;
+}
+
 __device__ __forceinline__ float group4_sum(float x) {
   x += __shfl_xor(x, 16, 64);
   return x + __shfl_xor(x, 32, 64);

@@ -51,6 +51,9 @@ CASES = [
     ("bf16_d256_causal", 1, 200, 200, 2, 2, 256, BF16, TL, 1.0),
     ("f16_d256_gqa2_ragged_noncausal", 2, 77, 130, 4, 2, 256, F16, NONE, 0.5),
     ("bf16_d256_bottom_right_long_q", 1, 150, 90, 2, 1, 256, BF16, BR, 1.0),
+    # rows that see few keys (top-left causal, N_K << N_Q), and D = 256 with a large scale: the
+    # fused stage 1's ddO subtracts dD O with dD summed over the bf16-rounded P ddS it multiplies
+    ("bf16_causal_few_keys_gqa", 2, 298, 34, 2, 1, 64, BF16, TL, 1.0),
     # fp32 at D = 128
     ("f32_d128_causal", 1, 160, 160, 2, 2, 128, F32, TL, 1.0),
     ("f32_d128_gqa2_ragged_noncausal", 2, 77, 130, 4, 2, 128, F32, NONE, 1.0),
@@ -77,6 +80,7 @@ SCALE_CASES = [
     ("f32_d128_causal_scale_0.3", 1, 100, 100, 2, 2, 128, F32, TL, 0.3),
     ("bf16_d256_causal_scale_0.0625", 1, 100, 100, 2, 2, 256, BF16, TL, 0.0625),
     ("bf16_d256_noncausal_scale_-0.05", 1, 100, 120, 2, 2, 256, BF16, NONE, -0.05),
+    ("bf16_d256_noncausal_scale_0.199", 2, 266, 239, 2, 2, 256, BF16, NONE, 0.199),
 ]
 SCALE_IDS = [c[0] for c in SCALE_CASES]
 

@@ -49,6 +49,12 @@ def _problems(count=36, seed=2024):
 
 PROBLEMS = _problems()
 
+# Two problems of a larger run of the same generator (250 problems, seed 7) whose ddO and dQ2 exceeded the
+# bf16 tolerance (2.000e-2 and 2.07e-2) before the fused stage 1 subtracted dD O with dD summed over the
+# bf16-rounded P ddS its ddO products take: rows that see few keys (N_K = 34 under a top-left mask), and
+# D = 256 with scale 0.199. A CPU model of the kernel's roundings puts them at 0.009 and 0.010 now.
+PROBLEMS += [("p44", 2, 266, 239, 2, 2, 256, BF16, 0, 0.199), ("p74", 2, 298, 34, 2, 1, 64, BF16, 1, None)]
+
 
 def _lse_err(lse, lse_ref):
     got, ref = to_np(lse), lse_ref
