@@ -254,14 +254,6 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
                : "memory");
 }
 
-// 4 bytes per lane from a per-lane 64-bit address.
-__device__ __forceinline__ void dma4(const void* gptr, uint32_t lds_byte_addr) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off"
-               :
-               : "v"(gptr), "{m0}"(lds_byte_addr)
-               : "memory");
-}
-
 // 4 bytes per lane, addressed as a uniform base plus a per-lane byte offset.
 __device__ __forceinline__ void dma4s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1"
