@@ -243,12 +243,24 @@ struct GroupCursor {
 // an SGPR and a vector-memory instruction that reads that SGPR. The second
 // arises whenever the compiler reloads a spilled SGPR of the scalar base with
 // v_readlane just before the statement; the load could then read the base's
-// previous contents (say, a saved exec mask) and fault. s_nop 4 gives five.
+// previous contents (say, a saved exec mask) and fault. s_nop 4 gives five;
+// the DMAs that follow one from the same base in a tile's sequence need only
+// the first.
 
 // 16 bytes per lane, addressed as a uniform 64-bit base (SGPR pair) plus a
 // per-lane 32-bit byte offset.
 __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
   asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "{m0}"(lds_byte_addr)
+               : "memory");
+}
+
+// dma16s directly after another dma16s from the same base: the base is already
+// settled, so only M0's wait state is needed (tests/test_dma_wait_states.py
+// checks the built code for a VALU write of any DMA base within five states).
+__device__ __forceinline__ void dma16s_next(const void* sbase, uint32_t voff, uint32_t lds_byte_addr) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
                : "v"(voff), "s"(sbase), "{m0}"(lds_byte_addr)
                : "memory");
@@ -289,8 +301,9 @@ template <typename T, int D, int COUNT = SwzTile<T, D>::kLoads, int SWZ = kSwzPa
   // lds_tile_addr (the tile's first byte) must be wave-uniform; gbase is the
   // tile's first row.
   __device__ __forceinline__ void issue(uint32_t lds_tile_addr, const void* gbase) const {
+    dma16s(gbase, voff[0], lds_tile_addr + 1024u * first);
 #pragma unroll
-    for (int i = 0; i < COUNT; ++i) dma16s(gbase, voff[i], lds_tile_addr + 1024u * (first + i));
+    for (int i = 1; i < COUNT; ++i) dma16s_next(gbase, voff[i], lds_tile_addr + 1024u * (first + i));
   }
 };
 
