@@ -110,7 +110,7 @@ fwd_kernel(FwdParams<T> p, int chunk) {
   };
 
   const float c2 = fabsf(p.scale) * kLog2e;  // > 0
-  constexpr float kRescale = 8.f;
+  constexpr float kBound = 256.f;  // 2^kRescale, kRescale = 8
   float m = -1e30f;  // running row max of the log2-domain logits (possibly stale, see below)
   float lpart = 0.f; // this lane's share of the running row sum
   f32x16 acc[DT];
@@ -144,31 +144,42 @@ fwd_kernel(FwdParams<T> p, int chunk) {
         for (int r = 0; r < 16; ++r)
           if (crow(r, g) > klim) S[r] = -INFINITY;
       }
-      float mloc = S[0];
+      // Lazy rescale: a row keeps its running maximum m (log2 units) while the
+      // probabilities it gives stay small, and O, l carry the same stale factor,
+      // which the final O / l and L = m + log2 l cancel. P is formed with the
+      // stale m first; if a lane's 16 values sum to more than 2^kRescale (or
+      // overflow: the first tile, with m = -1e30, always does), the wave takes
+      // the row maximum, rescales O and l to it and forms P again. So P <= 2^kRescale,
+      // and most tiles skip the maximum (15 max, a cross-lane exchange and a
+      // vote), the exp and the 33 multiplies of a rescale.
+      f32x16 P;
+      float psum = 0.f;
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, S[r]);
-      const float mnew = fmaxf(m, xgroup_max(mloc * c2));
-      // Lazy rescale: a row keeps its running maximum until it grows by more
-      // than kRescale (log2 units), so P <= 2^kRescale and O, l carry the same
-      // stale factor, which the final O / l and L = m + log2 l cancel. Most
-      // tiles then skip the exp and the 33 multiplies of a rescale.
-      if (__any(mnew > m + kRescale)) {
+      for (int r = 0; r < 16; ++r) {
+        P[r] = exp2_fast(fmaf(S[r], c2, -m));  // masked: exp2(-inf) = 0
+        psum += P[r];
+      }
+      if (__any(!(psum <= kBound))) {
+        float mloc = S[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, S[r]);
+        const float mnew = fmaxf(m, xgroup_max(mloc * c2));
         const float alpha = exp2_fast(m - mnew);
         lpart *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) acc[dt] *= alpha;
         m = mnew;
-      }
-      float psum = 0.f;
+        psum = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        S[r] = exp2_fast(fmaf(S[r], c2, -m));  // masked: exp2(-inf) = 0
-        psum += S[r];
+        for (int r = 0; r < 16; ++r) {
+          P[r] = exp2_fast(fmaf(S[r], c2, -m));
+          psum += P[r];
+        }
       }
       lpart += psum;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        const V8<T> oP = cvt8<T>(s ? hi8(S) : lo8(S));
+        const V8<T> oP = cvt8<T>(s ? hi8(P) : lo8(P));
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) acc[dt] = mma<T>(fr.trf(sa, kTile, dt, s), oP, acc[dt]);
       }
