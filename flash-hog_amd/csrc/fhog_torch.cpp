@@ -14,15 +14,30 @@
 // the Python exception class to raise for a non-zero status. _hip.py uses this
 // module when it is built and falls back to its own wrappers when it is not;
 // both reach the same kernels.
+//
+// attention() is dot_product_attention's eager autograd path in C++: two
+// torch::autograd::Function nodes with the rules of
+// flash_hog/torch/attention.py (the forward saving (q, k, v, L, O); its
+// backward, itself differentiable once, saving (q, k, v, O, L, dO); the double
+// backward with no cotangent for L and O), so that a Hessian-vector product
+// runs no Python between the autograd engine and the kernels.
+//
+// The calls themselves (the *_core functions) touch no Python object: the
+// autograd engine runs backward nodes on its own threads, without the GIL.
+// They throw ArgError and StatusError; the Python-facing functions release the
+// GIL around them and turn those into ValueError and the bound FlashHogError.
 #include <ATen/core/Tensor.h>
 #include <ATen/ops/empty.h>
 #include <ATen/ops/empty_like.h>
 #include <c10/core/DeviceGuard.h>
+#include <c10/core/GradMode.h>
 #include <c10/hip/HIPStream.h>
+#include <torch/csrc/autograd/custom_function.h>
 #include <torch/csrc/utils/pybind.h>
 
 #include <cstdint>
 #include <sstream>
+#include <stdexcept>
 #include <string>
 #include <tuple>
 
@@ -80,7 +95,17 @@ std::string device_str(const at::Tensor& t) {
   return os.str();
 }
 
-[[noreturn]] void value_error(const std::string& msg) { throw py::value_error(msg); }
+// A bad argument (ValueError in Python) and a non-zero C-ABI status
+// (FlashHogError(status, message) in Python).
+struct ArgError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+struct StatusError : std::runtime_error {
+  int status;
+  StatusError(int s, const std::string& msg) : std::runtime_error(msg), status(s) {}
+};
+
+[[noreturn]] void value_error(const std::string& msg) { throw ArgError(msg); }
 
 int dtype_code(at::ScalarType s) {
   switch (s) {
@@ -151,21 +176,21 @@ fhog_stream_t current_stream(const at::Tensor& t) {
   return c10::hip::getCurrentHIPStream(t.device().index()).stream();
 }
 
+// The message comes from the calling thread's fhog_last_error.
 void check_status(int status) {
   if (status == FHOG_OK) return;
   const Api& a = api();
   std::string msg = a.last_error();
   if (msg.empty()) msg = a.status_string(status);
-  PyErr_SetObject(a.error_cls.ptr(), py::make_tuple(status, msg).ptr());
-  throw py::error_already_set();
+  throw StatusError(status, msg);
 }
 
 void require_bound(const void* fn) {
   if (!fn) throw std::runtime_error("_fhog_torch.bind() has not been called");
 }
 
-std::tuple<at::Tensor, at::Tensor> attention_fwd(const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_,
-                                                 int causal, double scale) {
+std::tuple<at::Tensor, at::Tensor> fwd_core(const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_,
+                                            int causal, double scale) {
   require_bound((const void*)api().fwd);
   check_inputs({{"q", &q_}, {"k", &k_}, {"v", &v_}}, q_.scalar_type());
   const Dims d = dims(q_, k_);
@@ -174,18 +199,14 @@ std::tuple<at::Tensor, at::Tensor> attention_fwd(const at::Tensor& q_, const at:
   at::Tensor o = at::empty_like(q);
   at::Tensor lse = at::empty({(int64_t)d.B, (int64_t)d.N, (int64_t)d.Tq}, q.options().dtype(at::kFloat));
   c10::DeviceGuard guard(q.device());
-  int status;
-  {
-    py::gil_scoped_release nogil;
-    status = api().fwd(current_stream(q), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                       lse.data_ptr<float>(), d.B, d.Tq, d.Tk, d.N, d.Nk, d.H, dtype_code(q.scalar_type()),
-                       causal, (float)scale);
-  }
+  const int status = api().fwd(current_stream(q), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                               lse.data_ptr<float>(), d.B, d.Tq, d.Tk, d.N, d.Nk, d.H, dtype_code(q.scalar_type()),
+                               causal, (float)scale);
   check_status(status);
   return {o, lse};
 }
 
-std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> attention_bwd(
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> bwd_core(
     const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_, const at::Tensor& o_, const at::Tensor& dout_,
     const at::Tensor& lse_, int causal, double scale) {
   require_bound((const void*)api().bwd);
@@ -201,19 +222,16 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> attention_bwd(
   at::Tensor dq = at::empty_like(q), dk = at::empty_like(k), dv = at::empty_like(v);
   at::Tensor delta = at::empty({(int64_t)d.B, (int64_t)d.N, (int64_t)d.Tq}, q.options().dtype(at::kFloat));
   c10::DeviceGuard guard(q.device());
-  int status;
-  {
-    py::gil_scoped_release nogil;
-    status = api().bwd(current_stream(q), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(),
-                       lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr<float>(),
-                       d.B, d.Tq, d.Tk, d.N, d.Nk, d.H, dtype_code(q.scalar_type()), causal, (float)scale);
-  }
+  const int status =
+      api().bwd(current_stream(q), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dout.data_ptr(),
+                lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), delta.data_ptr<float>(), d.B,
+                d.Tq, d.Tk, d.N, d.Nk, d.H, dtype_code(q.scalar_type()), causal, (float)scale);
   check_status(status);
   return {dq, dk, dv, delta};
 }
 
 // dq2, dk2, dv2, ddo and the (3, B, N, Tq) fp32 row statistics D, dD, B.
-std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> attention_bwdbwd(
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> bwdbwd_core(
     const at::Tensor& q_, const at::Tensor& k_, const at::Tensor& v_, const at::Tensor& o_, const at::Tensor& dout_,
     const at::Tensor& ddq_, const at::Tensor& ddk_, const at::Tensor& ddv_, const at::Tensor& lse_, int causal,
     double scale) {
@@ -237,17 +255,133 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> attention
   float* st = stats.data_ptr<float>();
   const int64_t n_stat = (int64_t)d.B * d.N * d.Tq;
   c10::DeviceGuard guard(q.device());
-  int status;
-  {
-    py::gil_scoped_release nogil;
-    status = api().bwdbwd(current_stream(q), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                          dout.data_ptr(), ddq.data_ptr(), ddk.data_ptr(), ddv.data_ptr(), lse.data_ptr<float>(),
-                          dq2.data_ptr(), dk2.data_ptr(), dv2.data_ptr(), ddo.data_ptr(), st, st + n_stat,
-                          st + 2 * n_stat, d.B, d.Tq, d.Tk, d.N, d.Nk, d.H, dtype_code(q.scalar_type()), causal,
-                          (float)scale);
-  }
+  const int status = api().bwdbwd(current_stream(q), q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                  dout.data_ptr(), ddq.data_ptr(), ddk.data_ptr(), ddv.data_ptr(),
+                                  lse.data_ptr<float>(), dq2.data_ptr(), dk2.data_ptr(), dv2.data_ptr(),
+                                  ddo.data_ptr(), st, st + n_stat, st + 2 * n_stat, d.B, d.Tq, d.Tk, d.N, d.Nk, d.H,
+                                  dtype_code(q.scalar_type()), causal, (float)scale);
   check_status(status);
   return {dq2, dk2, dv2, ddo, stats};
+}
+
+// ------------------------------------------------------------------ autograd
+
+using torch::autograd::AutogradContext;
+using torch::autograd::variable_list;
+
+// Refuses a third derivative as the once_differentiable double backward of
+// flash_hog/torch/attention.py does. Under create_graph, with cotangents that
+// require grad, the double backward's results are detached, marked as
+// requiring grad and passed through this node (as copies), whose backward
+// raises: a backward() through them raises, while a grad() with respect to
+// the inputs finds no path through them.
+struct NoThirdOrder : public torch::autograd::Function<NoThirdOrder> {
+  static variable_list forward(AutogradContext*, const at::Tensor& dq2, const at::Tensor& dk2,
+                               const at::Tensor& dv2, const at::Tensor& ddo) {
+    return {dq2.clone(), dk2.clone(), dv2.clone(), ddo.clone()};
+  }
+  static variable_list backward(AutogradContext*, variable_list) {
+    throw std::runtime_error("trying to differentiate twice a function that was marked with @once_differentiable");
+  }
+};
+
+// Primal (q, k, v, O, L, dO) -> (dQ, dK, dV), differentiable once in q, k, v
+// and dO: _DotProductAttentionBwd (the rule
+// dot_product_attention_bwd_rule_fwd_rule and its rule
+// dot_product_attention_bwd_rule_bwd_rule).
+struct AttentionBwdFn : public torch::autograd::Function<AttentionBwdFn> {
+  static variable_list forward(AutogradContext* ctx, int64_t causal, double scale, const at::Tensor& q,
+                               const at::Tensor& k, const at::Tensor& v, const at::Tensor& lse, const at::Tensor& o,
+                               const at::Tensor& g) {
+    auto [dq, dk, dv, delta] = bwd_core(q, k, v, o, g, lse, (int)causal, scale);
+    ctx->save_for_backward({q, k, v, o, lse, g});
+    ctx->saved_data["causal"] = causal;
+    ctx->saved_data["scale"] = scale;
+    return {dq, dk, dv};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const variable_list r = ctx->get_saved_variables();  // q, k, v, O, L, dO
+    auto [dq2, dk2, dv2, ddo, stats] =
+        bwdbwd_core(r[0], r[1], r[2], r[3], r[5], grads[0], grads[1], grads[2], r[4],
+                    (int)ctx->saved_data["causal"].toInt(), ctx->saved_data["scale"].toDouble());
+    if (c10::GradMode::is_enabled() &&
+        (grads[0].requires_grad() || grads[1].requires_grad() || grads[2].requires_grad())) {
+      auto mark = [](const at::Tensor& t) { return t.detach().requires_grad_(true); };
+      const variable_list w = NoThirdOrder::apply(mark(dq2), mark(dk2), mark(dv2), mark(ddo));
+      dq2 = w[0], dk2 = w[1], dv2 = w[2], ddo = w[3];
+    }
+    // no cotangent for L and O (flash_hog/jax/_attention_impl.py:278-303)
+    return {at::Tensor(), at::Tensor(), dq2, dk2, dv2, at::Tensor(), at::Tensor(), ddo};
+  }
+};
+
+// Primal (q, k, v) -> (O, L), L not differentiable: _DotProductAttention (the
+// rule dot_product_attention_fwd_rule and its rule
+// dot_product_attention_bwd_rule, through AttentionBwdFn).
+struct AttentionFn : public torch::autograd::Function<AttentionFn> {
+  static variable_list forward(AutogradContext* ctx, const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                               int64_t causal, double scale) {
+    auto [o, lse] = fwd_core(q, k, v, (int)causal, scale);
+    ctx->save_for_backward({q, k, v, lse, o});
+    ctx->saved_data["causal"] = causal;
+    ctx->saved_data["scale"] = scale;
+    ctx->mark_non_differentiable({lse});
+    return {o, lse};
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    const variable_list r = ctx->get_saved_variables();  // q, k, v, L, O
+    // O enters the first backward as a constant: the double backward returns
+    // no cotangent for it, and detaching it keeps this node out of a second
+    // derivative's graph.
+    const variable_list d = AttentionBwdFn::apply(ctx->saved_data["causal"].toInt(),
+                                                  ctx->saved_data["scale"].toDouble(), r[0], r[1], r[2], r[3],
+                                                  r[4].detach(), grads[0]);
+    return {d[0], d[1], d[2], at::Tensor(), at::Tensor()};
+  }
+};
+
+// ----------------------------------------------------------- Python-facing
+
+// Runs f without the GIL and raises its errors as Python exceptions.
+template <class F>
+auto py_call(F&& f) {
+  try {
+    py::gil_scoped_release nogil;
+    return f();
+  } catch (const ArgError& e) {
+    throw py::value_error(e.what());
+  } catch (const StatusError& e) {
+    PyErr_SetObject(api().error_cls.ptr(), py::make_tuple(e.status, std::string(e.what())).ptr());
+    throw py::error_already_set();
+  }
+}
+
+std::tuple<at::Tensor, at::Tensor> attention_fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                                 int causal, double scale) {
+  require_bound((const void*)api().fwd);
+  return py_call([&] { return fwd_core(q, k, v, causal, scale); });
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> attention_bwd(
+    const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& o, const at::Tensor& dout,
+    const at::Tensor& lse, int causal, double scale) {
+  require_bound((const void*)api().bwd);
+  return py_call([&] { return bwd_core(q, k, v, o, dout, lse, causal, scale); });
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> attention_bwdbwd(
+    const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const at::Tensor& o, const at::Tensor& dout,
+    const at::Tensor& ddq, const at::Tensor& ddk, const at::Tensor& ddv, const at::Tensor& lse, int causal,
+    double scale) {
+  require_bound((const void*)api().bwdbwd);
+  return py_call([&] { return bwdbwd_core(q, k, v, o, dout, ddq, ddk, ddv, lse, causal, scale); });
+}
+
+// O of attention(q, k, v) with the autograd nodes above (when q, k or v
+// require grad and grad mode is on).
+at::Tensor attention(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, int64_t causal, double scale) {
+  require_bound((const void*)api().bwdbwd);
+  return py_call([&] { return AttentionFn::apply(q, k, v, causal, scale)[0]; });
 }
 
 }  // namespace
@@ -258,4 +392,5 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("attention_fwd", &attention_fwd);
   m.def("attention_bwd", &attention_bwd);
   m.def("attention_bwdbwd", &attention_bwdbwd);
+  m.def("attention", &attention, "attention(q, k, v, causal, scale) -> O, differentiable twice");
 }

@@ -18,6 +18,13 @@ rules compute total derivatives of (dQ, dK, dV) with respect to (q, k, v, dO).
 
 The rules are looked up as module attributes of _attention_impl at call time
 (attention.py:60, :70, :106, :115, :124), so they can be swapped at run time.
+
+Eager calls with the default rules, outside torch.func transforms and compiler
+traces, on plain GPU tensors, take the same two Functions written in C++
+(flash-hog_amd/csrc/fhog_torch.cpp, AttentionFn and AttentionBwdFn): the
+autograd engine then calls the kernels with no Python in between, which is
+what bounds a Hessian-vector product at short sequences. Their results are
+those of the Python Functions, bit for bit.
 """
 
 from __future__ import annotations
@@ -25,8 +32,27 @@ from __future__ import annotations
 import torch
 from torch.autograd.function import once_differentiable
 
-from flash_hog._types import MaskType
+from flash_hog import _hip
+from flash_hog._types import MaskType, causal_code
 from flash_hog.torch import _attention_impl as attn_impl
+
+# The rule bodies the C++ Functions reproduce; another one swapped in (a module
+# attribute of _attention_impl) sends calls through the Python Functions.
+_DEFAULT_RULES = (attn_impl.dot_product_attention_fwd_rule, attn_impl.dot_product_attention_bwd_rule,
+                  attn_impl.dot_product_attention_bwd_rule_fwd_rule, attn_impl.dot_product_attention_bwd_rule_bwd_rule)
+
+
+def _native_path(*tensors):
+    """The torch extension whose attention() serves this call with C++
+    autograd Functions, or None when the Python Functions must."""
+    if (torch._C._are_functorch_transforms_active() or torch.compiler.is_compiling()
+            or not all(type(t) is torch.Tensor and t.is_cuda for t in tensors)
+            or attn_impl.dot_product_attention_fwd_rule is not _DEFAULT_RULES[0]
+            or attn_impl.dot_product_attention_bwd_rule is not _DEFAULT_RULES[1]
+            or attn_impl.dot_product_attention_bwd_rule_fwd_rule is not _DEFAULT_RULES[2]
+            or attn_impl.dot_product_attention_bwd_rule_bwd_rule is not _DEFAULT_RULES[3]):
+        return None
+    return _hip.torch_ext()
 
 
 # Head dims the kernels take, per dtype. Another head dim up to the largest is
@@ -88,8 +114,12 @@ def dot_product_attention(query, key, value, is_causal: bool = False, scale: flo
     unbatched = query.ndim == 3
     if unbatched:
         query, key, value = query.unsqueeze(0), key.unsqueeze(0), value.unsqueeze(0)
-    fn = _DotProductAttention if torch._C._are_functorch_transforms_active() else _DotProductAttentionEager
-    result, _ = fn.apply(query, key, value, mask_type, float(scale))
+    native = _native_path(query, key, value)
+    if native is not None:
+        result = native.attention(query, key, value, causal_code(mask_type), float(scale))
+    else:
+        fn = _DotProductAttention if torch._C._are_functorch_transforms_active() else _DotProductAttentionEager
+        result, _ = fn.apply(query, key, value, mask_type, float(scale))
     if unbatched:
         result = result.squeeze(0)
     return result

@@ -79,6 +79,21 @@ def test_grad_of_grad_stops_at_second_order():
     assert not any(t.requires_grad for t in h)
 
 
+def test_native_path_only_for_plain_gpu_tensors():
+    """The C++ autograd Functions serve plain GPU tensors only: meta and CPU
+    tensors (and tensor subclasses) go through the Python Functions, whose
+    operators have the fake kernels used above."""
+    from flash_hog.torch import attention as att
+
+    assert att._native_path(meta(1, 8, 2, 64)) is None
+    assert att._native_path(torch.zeros(1, 8, 2, 64)) is None
+
+    class Sub(torch.Tensor):
+        pass
+
+    assert att._native_path(torch.zeros(1, 8, 2, 64).as_subclass(Sub)) is None
+
+
 def test_unbatched_shapes():
     q, k = meta(64, 4, 64), meta(80, 2, 64)
     assert attn(q, k, k).shape == q.shape
