@@ -156,7 +156,7 @@ bwd_q_kernel(BwdParams<T> p, int chunk) {
     if (kt + NST - 1 < nkt) issue(kt + NST - 1);
     if (kt < wkt) {
       const uint32_t sa = lds_kv + (uint32_t)(((uint32_t)kt % NST) * kStage);  // K at 0, V at kTile
-      f32x16 S = zero16(), u = u0;
+      f32x16 S = zero16(), u = u0;  // u: dP - D at D = 64, dP otherwise
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         S = mma<T>(fr.rowf(sa, 0, ks), qf[ks], S);

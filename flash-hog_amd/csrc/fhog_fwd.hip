@@ -110,7 +110,7 @@ fwd_kernel(FwdParams<T> p, int chunk) {
   };
 
   const float c2 = fabsf(p.scale) * kLog2e;  // > 0
-  constexpr float kBound = 256.f;  // 2^kRescale, kRescale = 8
+  constexpr float kBound = 256.f;  // bound on P (2^8)
   float m = -1e30f;  // running row max of the log2-domain logits (possibly stale, see below)
   float lpart = 0.f; // this lane's share of the running row sum
   f32x16 acc[DT];
@@ -147,11 +147,11 @@ fwd_kernel(FwdParams<T> p, int chunk) {
       // Lazy rescale: a row keeps its running maximum m (log2 units) while the
       // probabilities it gives stay small, and O, l carry the same stale factor,
       // which the final O / l and L = m + log2 l cancel. P is formed with the
-      // stale m first; if a lane's 16 values sum to more than 2^kRescale (or
-      // overflow: the first tile, with m = -1e30, always does), the wave takes
-      // the row maximum, rescales O and l to it and forms P again. So P <= 2^kRescale,
-      // and most tiles skip the maximum (15 max, a cross-lane exchange and a
-      // vote), the exp and the 33 multiplies of a rescale.
+      // stale m first. If a lane's 16 values sum to more than kBound, or
+      // overflow (the first tile, with m = -1e30, always does), the wave takes
+      // the row maximum, rescales O and l to it and forms P again; so
+      // P <= kBound. Most tiles thus skip the maximum (15 max and a cross-lane
+      // exchange) and the rescale (an exp and 33 multiplies).
       f32x16 P;
       float psum = 0.f;
 #pragma unroll
