@@ -55,6 +55,29 @@ def rel_err(a, r, floor: float = 0.0) -> float:
 DEGENERATE_FLOOR = 1e-2
 
 
+def b_stat_err(b, ref_d, ref_dd, ref_b) -> float:
+    """Error of the double backward's row statistic B on the scale it is used at.
+
+    B is scratch between the passes (TkBwdBwd returns it as such,
+    flash_hog/csrc/tk_bwdbwd/ffi.cu:79-98): pass 4 uses it only in
+    dS2 = P (dP2 - B) (flash_hog/jax/_pallas_gpu_kernel.py:247, 358), i.e.
+    through c = D dD + B. The fused stage 1 forms B as c - D dD with
+    c = <dO, ddO>, whose rounding is relative to |c|; where c and D dD nearly
+    cancel, B is small and that error is large relative to B alone. So
+    max|b - ref_b| is measured against max(max|ref_b|, max|c_ref|, floor).
+    """
+    b, ref_d, ref_dd, ref_b = (torch.as_tensor(t).double().cpu() for t in (b, ref_d, ref_dd, ref_b))
+    c_ref = ref_d * ref_dd + ref_b
+    den = max(ref_b.abs().max().item(), c_ref.abs().max().item(), DEGENERATE_FLOOR)
+    return (b - ref_b).abs().max().item() / den
+
+
+def stat_errs(got, ref):
+    """Relative errors of the statistics D, dD (rel_err) and B (b_stat_err)."""
+    return (rel_err(got[0], ref[0], DEGENERATE_FLOOR), rel_err(got[1], ref[1], DEGENERATE_FLOOR),
+            b_stat_err(got[2], ref[0], ref[1], ref[2]))
+
+
 def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
 

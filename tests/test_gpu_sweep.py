@@ -22,7 +22,7 @@ import random
 import pytest
 import torch
 
-from helpers import DEGENERATE_FLOOR, TOL, make_inputs, rel_err, to_np
+from helpers import DEGENERATE_FLOOR, TOL, make_inputs, rel_err, stat_errs, to_np
 from oracle import attention as ora
 
 pytestmark = pytest.mark.gpu
@@ -54,6 +54,11 @@ PROBLEMS = _problems()
 # bf16-rounded P ddS its ddO products take: rows that see few keys (N_K = 34 under a top-left mask), and
 # D = 256 with scale 0.199. A CPU model of the kernel's roundings puts them at 0.009 and 0.010 now.
 PROBLEMS += [("p44", 2, 266, 239, 2, 2, 256, BF16, 0, 0.199), ("p74", 2, 298, 34, 2, 1, 64, BF16, 1, None)]
+# A problem of a 250-problem run with seed 31 (its p07, inputs seeded with 108): one query row whose B is
+# the small difference of c = D dD + B = 0.284 and D dD = 0.269. The fused stage 1's B is then 17 % off
+# relative to B itself but 0.9 % of c, the scale at which pass 4 uses it (tests/helpers.py b_stat_err,
+# tests/test_rounding_model.py). All four outputs are within tolerance.
+PROBLEMS += [("s31p07", 1, 1, 78, 1, 1, 128, BF16, 0, 0.1247, 108)]
 
 
 def _lse_err(lse, lse_ref):
@@ -71,11 +76,12 @@ def _lse_err(lse, lse_ref):
 def test_random_problem_all_kernels(problem, cuda_device):
     from flash_hog import _hip
 
-    name, B, Nq, Nk, H, Hk, D, dtype, causal, scale = problem
+    name, B, Nq, Nk, H, Hk, D, dtype, causal, scale = problem[:10]
+    seed = problem[10] if len(problem) > 10 else 101 + int(name[1:])
     scale = D ** -0.5 if scale is None else scale
     print(f"[case] sweep {name}: B{B} Nq{Nq} Nk{Nk} H{H}/{Hk} D{D} {dtype} causal={causal} scale={scale}",
           flush=True)
-    x = make_inputs(B, Nq, Nk, H, D, dtype, seed=101 + int(name[1:]), kv_heads=Hk)
+    x = make_inputs(B, Nq, Nk, H, D, dtype, seed=seed, kv_heads=Hk)
     g = lambda t: t.to(cuda_device)
     tol = TOL[dtype]
 
@@ -105,6 +111,8 @@ def test_random_problem_all_kernels(problem, cuda_device):
     ref = ora.attn_bwd_bwd_stats(*(to_np(x[n]) for n in ("q", "k", "v")), to_np(o32), to_np(x["do"]),
                                  *(to_np(x[n]) for n in ("ddq", "ddk", "ddv")), to_np(l32), scale, causal,
                                  return_stats=True)
-    for a, r, label in zip((dq2, dk2, dv2, ddo) + tuple(stats), ref, ("dq2", "dk2", "dv2", "ddo", "D", "dD", "B")):
+    for a, r, label in zip((dq2, dk2, dv2, ddo), ref[:4], ("dq2", "dk2", "dv2", "ddo")):
         err = rel_err(a, r, DEGENERATE_FLOOR)
+        assert err < tol, f"{label}: rel err {err:.3e}"
+    for err, label in zip(stat_errs(tuple(stats), ref[4:]), ("D", "dD", "B")):
         assert err < tol, f"{label}: rel err {err:.3e}"

@@ -1,4 +1,5 @@
-"""A CPU model of the fused stage 1's operand roundings, for its ddO epilogue.
+"""A CPU model of the fused stage 1's operand roundings, for its ddO epilogue
+and its row statistic B.
 
 The fused stage 1 (flash-hog_amd/csrc/fhog_bwdbwd_fused.hip) accumulates
 ddO = sum_j P ddV + sum_j x V - dD O in one sweep, x = P ddS, where the
@@ -57,3 +58,32 @@ def test_rounded_dd_halves_the_ddo_error_where_rows_see_few_keys():
     assert errs[False] > 1.5e-2, errs  # the unrounded dD: at the bf16 tolerance
     assert errs[True] < 1e-2, errs     # the kernel's rounded dD
     assert errs[True] < 0.6 * errs[False], errs
+
+
+def test_b_statistic_error_is_at_the_scale_of_c():
+    """The fused stage 1 forms the row statistic B as c - D dD with
+    c = <dO, ddO>, ddO accumulated from P and P ddS rounded to bf16. On the
+    problem of tests/test_gpu_sweep.py s31p07 (one query row, N_K 78, D 128,
+    scale 0.1247), c = 0.284 and D dD = 0.269 nearly cancel: the model's B is
+    far off relative to B (which is why tests/helpers.py b_stat_err measures
+    it against |c|), and within 1e-2 of |c|, the scale at which pass 4 uses it
+    (dS2 = P (dP2 - B), flash_hog/jax/_pallas_gpu_kernel.py:358)."""
+    B, Nq, Nk, H, D, scale = 1, 1, 78, 1, 128, 0.1247
+    x = make_inputs(B, Nq, Nk, H, D, torch.bfloat16, seed=108)
+    o_ref, lse = ora.attn_fwd(to_np(x["q"]), to_np(x["k"]), to_np(x["v"]), scale, 0)
+    o = _bf16(o_ref)
+    lse = lse.astype(np.float32).astype(np.float64)
+    ref = ora.attn_bwd_bwd_stats(*(to_np(x[n]) for n in ("q", "k", "v")), o, to_np(x["do"]),
+                                 *(to_np(x[n]) for n in ("ddq", "ddk", "ddv")), lse, scale, 0, return_stats=True)
+    d_ref, dd_ref, b_ref = (float(r[0, 0, 0]) for r in ref[4:])
+    q, do, ddq, k, v, ddk, ddv = (to_np(x[n])[0, :, 0] for n in ("q", "do", "ddq", "k", "v", "ddk", "ddv"))
+    p = np.exp(scale * q @ k.T - lse[0, 0][:, None])
+    xs = p * scale * (ddq @ k.T + q @ ddk.T)
+    d = float((o[0, :, 0] * do).sum())
+    dd = float(xs.sum())
+    ddo = _bf16(p) @ ddv + _bf16(xs) @ v - _bf16(xs).sum(-1)[:, None] * o[0, :, 0]
+    b_model = float((do * ddo).sum()) - d * dd
+    c_ref = d_ref * dd_ref + b_ref
+    assert abs(c_ref) > 10 * abs(b_ref)
+    assert abs(b_model - b_ref) > 0.1 * abs(b_ref)
+    assert abs(b_model - b_ref) < 1e-2 * abs(c_ref)
