@@ -48,7 +48,7 @@ typedef struct ihipStream_t* fhog_stream_t;
 enum fhog_status {
   FHOG_OK = 0,
   FHOG_ERR_INVALID_ARGUMENT = 1, /* null/misaligned pointer, bad size, bad enum */
-  FHOG_ERR_UNSUPPORTED = 2,      /* valid request this build has no kernel for */
+  FHOG_ERR_UNSUPPORTED = 2,      /* valid request the library has no kernel for */
   FHOG_ERR_LAUNCH = 3            /* the HIP runtime rejected a kernel launch */
 };
 

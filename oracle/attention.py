@@ -1,7 +1,7 @@
 """CPU oracle for the Flash-HOG attention path (numpy, float64).
 
 TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
-cpu_baseline leg may import this module, and only as the checker or the
+cpu_baseline leg may import this module, and only to check results or as the
 timed CPU baseline; the product path never calls it.
 
 It restates the reference's equations with a materialised (N_Q, N_K) score

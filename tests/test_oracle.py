@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/attention.py) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/attention.py) before the GPU tests compare against it.
 
 Each oracle function is checked against something other than its own formula:
 the reference's golden vectors, finite differences, torch autograd (a library
