@@ -12,10 +12,15 @@
 //   dQ2 = scale (sum_j P u ddK + sum_j X K - dD sum_j P u K - c sum_j P K),
 //   ddO = sum_j P ddV + sum_j x V - dD O,                c = D dD + B,
 // because P (dP2 - B) = X - dD P u - c P, ddP = x - dD P and sum_j P V = O.
-// The row statistic needs no per-pair work either: expanding B's definition
-// (flash_hog/jax/_pallas_gpu_kernel.py:209-210),
-//   c = D dD + B = sum_j P dPa + sum_j x dP - dD sum_j P dP = <dO, ddO>,
-// since dPa = dO ddV^T and dP = dO V^T. Every key tile is streamed once; per
+// The row statistic comes from two more per-pair sums: summing
+// P (dP2 - B) = X - dD P u - c P over the keys (sum_j P = 1, and B is
+// sum_j P dP2, flash_hog/jax/_pallas_gpu_kernel.py:209-210) gives
+//   c = sum_j X - dD sum_j P u,   B = c - D dD,
+// both sums taken over the fp32 values before any rounding. (c also equals
+// <dO, ddO>, but ddO accumulates P and x rounded to T, and the subtraction
+// D dD cancels most of c, so that form left B off by up to 1e-2 of |c|: at
+// D = 256 with four queries that put dK2 at 2.2e-2 of its largest entry.)
+// Every key tile is streamed once; per
 // tile a wave forms the five score products (S, ddS twice, dP, dPa), one exp
 // per pair, and six output products into four accumulators (dQ2 part,
 // sum P u K, sum P K, ddO part). The dP accumulator starts at -D, so it ends
@@ -201,6 +206,8 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   for (int db = 0; db < DB; ++db) acc_a[db] = acc_s[db] = acc_p[db] = acc_o[db] = zero4();
   float dd_acc = 0.f;  // dD = sum P ddS over this lane's keys
   float ddr_acc = 0.f;  // the same sum over P ddS rounded to T, as the ddO products take it
+  float xs_acc = 0.f;   // sum X over this lane's keys
+  float pu_acc = 0.f;   // sum P u over this lane's keys
   const f32x4 init_u = {nD, nD, nD, nD};
 
   // Score tiles of the key tile in slot sa (K at 0, V at kTile, ddK at
@@ -240,6 +247,8 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
       vx[e] = x;
       vu[e] = P * u;                              // P u
       vX[e] = fmaf(x, u, P * sc.dPa[kb][i]);      // P (dPa + ddS u)
+      xs_acc += vX[e];
+      pu_acc += vu[e];
     }
     const V8<T> oP = cvt8<T>(vP), ox = cvt8<T>(vx), ou = cvt8<T>(vu), oX = cvt8<T>(vX);
     ddr_acc = add_sum8<T>(ox, ddr_acc);
@@ -328,29 +337,25 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   const float dDo = group4_sum(ddr_acc);
   // A row that sees exactly one key (see above).
   const bool one_key = (CAUSAL ? min(p.nk, qi + p.coff + 1) : p.nk) == 1;
-  // ddO = acc_o - dD O and c = <dO, ddO>, from this lane's four columns of
-  // each 16-column block (16 db + 4 g + i), summed over the four lane groups.
+  // c = D dD + B from the unrounded per-pair sums (see above).
+  const float c = group4_sum(xs_acc) - dD * group4_sum(pu_acc);
+  // ddO = acc_o - dD O, from this lane's four columns of each 16-column block
+  // (16 db + 4 g + i).
   const long roff = qbase + (long)qi * rs;
   f32x4 y[DB];
-  float cpart = 0.f;
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
     const int d = 16 * db + 4 * g;
-    V4<T> ov, dov;
+    V4<T> ov;
     if (qvalid) {
       ov = *reinterpret_cast<const V4<T>*>(p.o + roff + d);
-      dov = *reinterpret_cast<const V4<T>*>(p.dout + roff + d);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ov[i] = dov[i] = (T)0.0f;
+      for (int i = 0; i < 4; ++i) ov[i] = (T)0.0f;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      y[db][i] = acc_o[db][i] - dDo * (float)ov[i];
-      cpart = fmaf((float)dov[i], y[db][i], cpart);
-    }
+    for (int i = 0; i < 4; ++i) y[db][i] = acc_o[db][i] - dDo * (float)ov[i];
   }
-  const float c = group4_sum(cpart);
   const float Bi = c - Di * dD;
   if (qvalid) {
     if (g == 0) {

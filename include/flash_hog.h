@@ -123,11 +123,9 @@ int fhog_attention_bwd(fhog_stream_t stream,
  * (as flash_bwdbwd0 does at _pallas_gpu_kernel.py:110) and written to delta.
  * delta, ddelta, bstat: caller-owned workspace, fhog_row_stat_bytes each;
  * on return they hold D, dD and B. Like TkBwdBwd's dD and B they are
- * scratch between the two passes: pass 4 uses B only through
- * c = D dD + B, and for 2-byte types B is formed as c - D dD with c the
- * dot product of dO and ddO, so its absolute error is at the rounding of
- * c (about 1e-2 of |c| at most), which is large relative to B itself
- * where c and D dD nearly cancel.
+ * scratch between the two passes (pass 4 uses B through c = D dD + B); B
+ * is summed from unrounded per-pair terms, so it holds where c and D dD
+ * nearly cancel.
  * Two kernels are enqueued on stream; the second reads the statistics the
  * first writes.
  */

@@ -61,10 +61,11 @@ def b_stat_err(b, ref_d, ref_dd, ref_b) -> float:
     B is scratch between the passes (TkBwdBwd returns it as such,
     flash_hog/csrc/tk_bwdbwd/ffi.cu:79-98): pass 4 uses it only in
     dS2 = P (dP2 - B) (flash_hog/jax/_pallas_gpu_kernel.py:247, 358), i.e.
-    through c = D dD + B. The fused stage 1 forms B as c - D dD with
-    c = <dO, ddO>, whose rounding is relative to |c|; where c and D dD nearly
-    cancel, B is small and that error is large relative to B alone. So
-    max|b - ref_b| is measured against max(max|ref_b|, max|c_ref|, floor).
+    through c = D dD + B, so its error matters on the scale of c: where c
+    and D dD nearly cancel, B is small, and an error the size of c's
+    rounding (as in the two-sweep fp32 stage 1, B = r1 - dD r2 - D dD + r3)
+    is large relative to B alone. So max|b - ref_b| is measured against
+    max(max|ref_b|, max|c_ref|, floor).
     """
     b, ref_d, ref_dd, ref_b = (torch.as_tensor(t).double().cpu() for t in (b, ref_d, ref_dd, ref_b))
     c_ref = ref_d * ref_dd + ref_b

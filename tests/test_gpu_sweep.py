@@ -59,6 +59,10 @@ PROBLEMS += [("p44", 2, 266, 239, 2, 2, 256, BF16, 0, 0.199), ("p74", 2, 298, 34
 # relative to B itself but 0.9 % of c, the scale at which pass 4 uses it (tests/helpers.py b_stat_err,
 # tests/test_rounding_model.py). All four outputs are within tolerance.
 PROBLEMS += [("s31p07", 1, 1, 78, 1, 1, 128, BF16, 0, 0.1247, 108)]
+# A problem of a 250-problem run with seed 79 (its p08, inputs seeded with 109): four queries, D = 256,
+# bottom-right mask. B formed as <dO, ddO> - D dD put dK2 at 2.21e-2 against the 2e-2 bar; with B summed
+# from unrounded per-pair terms it is within tolerance (tests/test_rounding_model.py).
+PROBLEMS += [("s79p08", 1, 4, 201, 3, 3, 256, BF16, 2, 0.1843, 109)]
 
 
 def _lse_err(lse, lse_ref):
