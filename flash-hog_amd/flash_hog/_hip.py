@@ -25,6 +25,7 @@ import importlib.util
 import os
 import pathlib
 import sysconfig
+import warnings
 
 import torch
 
@@ -90,18 +91,26 @@ TORCH_EXT_PATH = LIB_PATH.parent / ("_fhog_torch" + sysconfig.get_config_var("EX
 @functools.cache
 def torch_ext():
     """The _fhog_torch extension bound to lib()'s entry points, or None when it
-    is not built (or FLASH_HOG_TORCH_EXT=0): the Python wrappers then do the
-    same work."""
+    is not built, cannot be loaded (built for another torch or Python, an
+    undefined symbol: a warning says why, once) or FLASH_HOG_TORCH_EXT=0; the
+    Python wrappers then do the same work. A missing kernel library is still
+    an error (lib() raises), since the wrappers need it too. The result,
+    None included, is cached."""
     if os.environ.get(TORCH_EXT_ENV, "1") == "0" or not TORCH_EXT_PATH.exists():
         return None
-    name = "flash_hog._lib._fhog_torch"
-    loader = importlib.machinery.ExtensionFileLoader(name, str(TORCH_EXT_PATH))
-    mod = importlib.util.module_from_spec(importlib.util.spec_from_loader(name, loader))
-    loader.exec_module(mod)
     L = lib()
-    addr = lambda fn: ctypes.cast(fn, ctypes.c_void_p).value
-    mod.bind(addr(L.fhog_attention_fwd), addr(L.fhog_attention_bwd), addr(L.fhog_attention_bwdbwd),
-             addr(L.fhog_last_error), addr(L.fhog_status_string), FlashHogError)
+    name = "flash_hog._lib._fhog_torch"
+    try:
+        loader = importlib.machinery.ExtensionFileLoader(name, str(TORCH_EXT_PATH))
+        mod = importlib.util.module_from_spec(importlib.util.spec_from_loader(name, loader))
+        loader.exec_module(mod)
+        addr = lambda fn: ctypes.cast(fn, ctypes.c_void_p).value
+        mod.bind(addr(L.fhog_attention_fwd), addr(L.fhog_attention_bwd), addr(L.fhog_attention_bwdbwd),
+                 addr(L.fhog_last_error), addr(L.fhog_status_string), FlashHogError)
+    except (ImportError, OSError, AttributeError) as exc:
+        warnings.warn(f"Flash-HOG torch extension {TORCH_EXT_PATH} not loaded ({exc}); "
+                      "using the Python wrappers", RuntimeWarning, stacklevel=2)
+        return None
     return mod
 
 

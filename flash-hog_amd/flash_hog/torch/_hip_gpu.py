@@ -234,6 +234,8 @@ def supported(*, is_causal: bool, seq_len: int, head_dim: int, num_q_heads: int,
     count as supported. Nothing is launched or allocated."""
     if causal_alignment not in ("top_left", "bottom_right"):
         raise ValueError(f"causal_alignment must be 'top_left' or 'bottom_right', got {causal_alignment!r}")
+    if head_dim < 1:
+        return False  # no kernel takes it, and it has no default scale
     try:
         if device is None:
             if not torch.cuda.is_available():
@@ -246,7 +248,7 @@ def supported(*, is_causal: bool, seq_len: int, head_dim: int, num_q_heads: int,
                 MaskType.CAUSAL if causal_alignment == "top_left" else MaskType.CAUSAL_BOTTOM_RIGHT)
         from flash_hog.torch.attention import kernel_head_dim
 
-        kernel_dim = kernel_head_dim(dtype, head_dim) if head_dim >= 1 else None
+        kernel_dim = kernel_head_dim(dtype, head_dim)
         ok, _ = _hip.attention_supported(batch, seq_len, seq_len if kv_seq_len is None else kv_seq_len, num_q_heads,
                                          num_kv_heads, head_dim if kernel_dim is None else kernel_dim, dtype,
                                          causal_code(mask), head_dim ** -0.5 if scale is None else scale,

@@ -123,9 +123,14 @@ int fhog_attention_bwd(fhog_stream_t stream,
  * (as flash_bwdbwd0 does at _pallas_gpu_kernel.py:110) and written to delta.
  * delta, ddelta, bstat: caller-owned workspace, fhog_row_stat_bytes each;
  * on return they hold D, dD and B. Like TkBwdBwd's dD and B they are
- * scratch between the two passes (pass 4 uses B through c = D dD + B); B
- * is summed from unrounded per-pair terms, so it holds where c and D dD
- * nearly cancel.
+ * scratch between the two passes (pass 4 uses B through c = D dD + B).
+ * Accuracy: D, dD and B are fp32 sums of fp32 per-pair terms (2-byte types:
+ * B = sum_j X_j - dD (sum_j P_j u_j + D), the per-pair form; fp32:
+ * B = r1 - dD r2 - D dD + r3). Over a call each is within the dtype's
+ * tolerance of its exact value relative to its own largest entry. Per row,
+ * B = c - D dD is a difference that any formula for it must take, so a row
+ * whose B is much smaller than its D dD holds B only to about 1e-7 |c|
+ * (fp32 rounding of c), not to 1e-7 |B|.
  * Two kernels are enqueued on stream; the second reads the statistics the
  * first writes.
  */
@@ -168,8 +173,8 @@ int fhog_attention_bwdbwd_stage(fhog_stream_t stream, int stage,
  * bit. It calls no allocating routine, for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops, harnesses
  * that forbid hipMalloc); the first call on a device looks up the array's
- * address there once. It has no counterpart in the reference, whose handler
- * receives its scratch from XLA (ffi.cu:79-98). Every call on a device shares
+ * address there once. It has no counterpart in the reference; it is for
+ * callers that cannot allocate. Every call on a device shares
  * that device's array: calls that overlap on one device (concurrent streams)
  * race on it and must be serialised by the caller.
  */

@@ -206,6 +206,39 @@ def test_supported_python_api_without_gpu():
     assert not ok and "dtype" in why
     with pytest.raises(ValueError, match="causal_alignment"):
         flash_hog.supported(**kw, causal_alignment="diagonal")
+    # head_dim < 1 has no default scale (0 ** -0.5): False, even with a device named
+    for hd in (0, -64):
+        assert flash_hog.supported(**{**kw, "head_dim": hd}, device=0) is False
+        assert flash_hog.supported(**{**kw, "head_dim": hd}) is False
+
+
+def test_unloadable_torch_extension_falls_back(monkeypatch, tmp_path):
+    """An extension file that exists but cannot be loaded (built for another
+    torch or Python) gives one warning and the Python wrappers, not an error
+    from every call; the result is cached, so the load is not retried."""
+    import warnings
+
+    import torch
+
+    from flash_hog import _hip
+
+    bad = tmp_path / _hip.TORCH_EXT_PATH.name
+    bad.write_bytes(b"\x7fELF but not a shared object")
+    monkeypatch.setattr(_hip, "TORCH_EXT_PATH", bad)
+    _hip.torch_ext.cache_clear()
+    try:
+        with pytest.warns(RuntimeWarning, match="not loaded"):
+            assert _hip.torch_ext() is None
+        with warnings.catch_warnings():
+            warnings.simplefilter("error")
+            assert _hip.torch_ext() is None
+        # the capability query and the Python wrappers' checks still run
+        assert _hip.attention_supported(4, 2048, 2048, 16, 16, 64, torch.bfloat16, True, 0.125) == (True, "")
+        q = torch.zeros(1, 8, 2, 64, dtype=torch.bfloat16)
+        with pytest.raises(ValueError, match="must be on a GPU device"):
+            _hip.attention_fwd(q, q, q, 1, 0.125)
+    finally:
+        _hip.torch_ext.cache_clear()
 
 
 def test_torch_extension_is_built_and_bound():

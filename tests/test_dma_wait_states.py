@@ -10,9 +10,11 @@ states, which fhog_device.h puts in each statement as an s_nop:
 A DMA whose base was read stale faulted the GPU now and then. This test
 disassembles the gfx950 code objects of the library built here and checks that
 every LDS DMA directly follows an s_nop (five wait states for a scalar base,
-unless the DMA just before it used the same base), and that no DMA with a
+unless the DMA just before it used the same base), that no DMA with a
 scalar base has a VALU write of that base within the five preceding wait
-states (a straight-line scan). CPU only.
+states (a straight-line scan), and that M0 is written by an SALU instruction
+in the DMA's own block: the statement's single wait state covers only that
+(a v_readfirstlane into M0 would need five). CPU only.
 """
 
 from __future__ import annotations
@@ -150,3 +152,25 @@ def test_no_dma_base_written_by_valu_within_five_states(listing):
                 states += 1
                 if states >= 5:
                     break
+
+
+def test_m0_of_every_lds_dma_is_written_by_salu_in_its_block(listing):
+    """The last write of M0 before each DMA is in the same straight-line code
+    (no branch target in between) and is an SALU instruction."""
+    seen = 0
+    for name, ins in listing:
+        for i, t in enumerate(ins):
+            if not t.startswith("global_load_lds"):
+                continue
+            seen += 1
+            writer = None
+            for j in range(i - 1, -1, -1):
+                if ins[j] == LABEL:
+                    break
+                op, *rest = ins[j].replace(",", " ").split()
+                if rest and rest[0] == "m0":
+                    writer = op
+                    break
+            assert writer is not None, (name, i, "M0 written in another block", ins[max(0, i - 8):i + 1])
+            assert writer.startswith("s_"), (name, i, writer, t)
+    assert seen > 1000, seen
