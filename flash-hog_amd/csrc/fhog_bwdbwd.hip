@@ -39,6 +39,8 @@
 // the same eighth of the (batch, head) pairs at every rank, so the blocks that
 // stream one (batch, head) share one L2.
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "fhog_device.h"
@@ -634,13 +636,27 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
 
 }  // namespace
 
+// Stage 1 for 2-byte types at D = 64 runs the fused kernel (16 queries per
+// wave, two waves per SIMD) unless FLASH_HOG_STAGE1=q32 selects the kernel
+// with 32 queries per wave at one wave per SIMD and a hand-scheduled sweep
+// (fhog_bwdbwd_q32.hip). Both give the same results to rounding; at
+// B4 N2048 H16 D64 causal bf16 the fused kernel is about 4 % faster. Read at
+// every launch, so a process can switch between them.
+inline bool stage1_q32_selected() {
+  const char* v = std::getenv("FLASH_HOG_STAGE1");
+  return v != nullptr && std::strcmp(v, "q32") == 0;
+}
+
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stages) {
   const int nqb = (p.nq + 32 * kWaves - 1) / (32 * kWaves);
   const int nkb = (p.nk + 32 * kWaves - 1) / (32 * kWaves);
   if (stages & 1) {
     hipError_t e;
-    if constexpr (sizeof(T) == 2) {
+    if constexpr (sizeof(T) == 2 && D == 64) {
+      e = stage1_q32_selected() ? launch_bwdbwd_stage1_q32<T, CAUSAL>(p, stream)
+                                : launch_bwdbwd_stage1_fused<T, D, CAUSAL>(p, stream);
+    } else if constexpr (sizeof(T) == 2) {
       e = launch_bwdbwd_stage1_fused<T, D, CAUSAL>(p, stream);
     } else {
       const int npairs = p.batch * p.heads;

@@ -121,43 +121,6 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   const int qi = q0 + n;
   const bool qvalid = qi < p.nq;
 
-  // Query-side operands (B of the score products) and D_i = <O_i, dO_i>.
-  V8<T> qf[KS], ddqf[KS], dof[KS];
-  float dpart = 0.f;
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    const long off = qbase + (long)qi * rs + 32 * ks + 8 * g;
-    if (qvalid) {
-      qf[ks] = *reinterpret_cast<const V8<T>*>(p.q + off);
-      ddqf[ks] = *reinterpret_cast<const V8<T>*>(p.ddq + off);
-      dof[ks] = *reinterpret_cast<const V8<T>*>(p.dout + off);
-      const V8<T> of = *reinterpret_cast<const V8<T>*>(p.o + off);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dpart += (float)of[e] * (float)dof[ks][e];
-    } else {
-      qf[ks] = zero8<T>();
-      ddqf[ks] = zero8<T>();
-      dof[ks] = zero8<T>();
-    }
-  }
-  const float scale = p.scale;
-  if constexpr (PRE) {
-    // scale is a power of two: Q and ddQ carry it exactly, so S and ddS come
-    // out of the matrix products already scaled (bit-identical to scaling them
-    // afterwards) and the element-wise step skips one multiply.
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        qf[ks][e] = (T)((float)qf[ks][e] * scale);
-        ddqf[ks][e] = (T)((float)ddqf[ks][e] * scale);
-      }
-  }
-  const float c2 = PRE ? kLog2e : scale * kLog2e;
-  const float Di = group4_sum(dpart);
-  const float nD = -Di;
-  const float nL2 = qvalid ? -p.lse[sbase + qi] * kLog2e : 0.f;
-
   // Keys [0, kend) are visible to some query of the workgroup, [0, wend) to
   // some query of this wave.
   int kend = p.nk;
@@ -179,10 +142,6 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   dma.init(row_bytes, BK, lane);
   const uint32_t lds_kv = lds_base_u32(s_kv);
   const uint32_t lds_wave = lds_kv + wave * kTile;
-  // Retire the query-side loads before the ring starts: vmcnt counts the
-  // untracked LDS DMAs too, so a wait for them inside the loop would drain the
-  // prefetched tiles.
-  wait_vmem();
   auto issue = [&](int kt) {
     const int nvalid = p.nk - kt * BK;
     const uint32_t dst = lds_wave + (uint32_t)(((uint32_t)kt % NST) * kStage);
@@ -196,10 +155,61 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
       part.issue(dst, gsrc);
     }
   };
+  // The ring's first NST - 1 tiles: all but the last go out before the
+  // query-side loads and the last once the query side has been used. The
+  // compiler does not count the LDS DMAs (they are inline assembly), so its
+  // waits for the query side also wait for every DMA issued before them; the
+  // loop's own waits count DMAs and are only made stricter by older loads.
   int hi = -1;  // last tile issued
 #pragma unroll
-  for (int i = 0; i < NST - 1; ++i)
+  for (int i = 0; i < NST - 2; ++i)
     if (i < nkt) issue(++hi);
+
+  // Query-side operands (B of the score products), D_i = <O_i, dO_i> and the
+  // logsumexp, in one batch of loads. A lane past the last query loads the
+  // last query's row: its own results are never stored, and a matrix product
+  // column or row sum of one query never mixes in another's, so finite
+  // values are all it needs.
+  const long roff = qbase + (long)min(qi, p.nq - 1) * rs;
+  V8<T> qf[KS], ddqf[KS], dof[KS], of[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const long off = roff + 32 * ks + 8 * g;
+    qf[ks] = *reinterpret_cast<const V8<T>*>(p.q + off);
+    ddqf[ks] = *reinterpret_cast<const V8<T>*>(p.ddq + off);
+    dof[ks] = *reinterpret_cast<const V8<T>*>(p.dout + off);
+    of[ks] = *reinterpret_cast<const V8<T>*>(p.o + off);
+  }
+  const float lse = p.lse[sbase + min(qi, p.nq - 1)];
+  float dpart = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dpart += (float)of[ks][e] * (float)dof[ks][e];
+  const float scale = p.scale;
+  if constexpr (PRE) {
+    // scale is a power of two: Q and ddQ carry it exactly, so S and ddS come
+    // out of the matrix products already scaled (bit-identical to scaling them
+    // afterwards) and the element-wise step skips one multiply.
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        qf[ks][e] = (T)((float)qf[ks][e] * scale);
+        ddqf[ks][e] = (T)((float)ddqf[ks][e] * scale);
+      }
+  }
+  const float c2 = PRE ? kLog2e : scale * kLog2e;
+  const float Di = group4_sum(dpart);
+  const float nD = -Di;
+  const float nL2 = -lse * kLog2e;
+  // Everything the loop takes from the query side is final before the last
+  // prologue tile is issued (the empty statements pin the order, and the
+  // memory clobber keeps the loads above them).
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(qf[ks]), "v"(ddqf[ks]), "v"(dof[ks]));
+  asm volatile("" ::"v"(nD), "v"(nL2) : "memory");
+  if (NST - 2 < nkt) issue(++hi);
 
   f32x4 acc_a[DB], acc_s[DB], acc_p[DB], acc_o[DB];
 #pragma unroll
@@ -341,20 +351,13 @@ bwdbwd_q_fused_kernel(BwdBwdParams<T> p, int chunk) {
   const float c = group4_sum(xs_acc) - dD * group4_sum(pu_acc);
   // ddO = acc_o - dD O, from this lane's four columns of each 16-column block
   // (16 db + 4 g + i).
-  const long roff = qbase + (long)qi * rs;
   f32x4 y[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
     const int d = 16 * db + 4 * g;
-    V4<T> ov;
-    if (qvalid) {
-      ov = *reinterpret_cast<const V4<T>*>(p.o + roff + d);
-    } else {
+    const V4<T> o4 = *reinterpret_cast<const V4<T>*>(p.o + roff + d);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ov[i] = (T)0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) y[db][i] = acc_o[db][i] - dDo * (float)ov[i];
+    for (int i = 0; i < 4; ++i) y[db][i] = acc_o[db][i] - dDo * (float)o4[i];
   }
   const float Bi = c - Di * dD;
   if (qvalid) {

@@ -79,6 +79,13 @@ template <typename T> __device__ __forceinline__ V8<T> zero8() {
   return z;
 }
 
+template <typename T> __device__ __forceinline__ V8<T> ones8() {
+  V8<T> z;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) z[e] = (T)1.0f;
+  return z;
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll

@@ -65,6 +65,10 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t s, int stages = 3
 // Stage 1 in one sweep (2-byte types, D = 64 and 128); launch_bwdbwd selects it.
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd_stage1_fused(const BwdBwdParams<T>& p, hipStream_t s);
+// Stage 1 with 32 queries per wave at one wave per SIMD (2-byte types, D = 64);
+// launch_bwdbwd selects it.
+template <typename T, bool CAUSAL>
+hipError_t launch_bwdbwd_stage1_q32(const BwdBwdParams<T>& p, hipStream_t s);
 // Stage 2 with 16 keys per wave (2-byte types, D = 128); launch_bwdbwd selects it.
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd_stage2_k16(const BwdBwdParams<T>& p, hipStream_t s);
