@@ -647,6 +647,16 @@ inline bool stage1_q32_selected() {
   return v != nullptr && std::strcmp(v, "q32") == 0;
 }
 
+// Stage 2 for bf16 at D = 64 runs bwdbwd_k_kernel below (32 keys per wave,
+// two waves per SIMD) unless FLASH_HOG_STAGE2=k32 selects the kernel with a
+// generated sweep at one wave per SIMD (fhog_bwdbwd_k32.hip). Both give the
+// same results to rounding; at B4 N2048 H16 D64 causal bf16 the compiled
+// kernel is about 10 % faster. Read at every launch.
+inline bool stage2_k32_selected() {
+  const char* v = std::getenv("FLASH_HOG_STAGE2");
+  return v != nullptr && std::strcmp(v, "k32") == 0;
+}
+
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stages) {
   const int nqb = (p.nq + 32 * kWaves - 1) / (32 * kWaves);
@@ -670,6 +680,9 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stage
     if constexpr (sizeof(T) == 2 && D >= 128) {
       return launch_bwdbwd_stage2_k16<T, D, CAUSAL>(p, stream);
     } else {
+      if constexpr (std::is_same_v<T, __bf16> && D == 64) {
+        if (stage2_k32_selected()) return launch_bwdbwd_stage2_k32<CAUSAL>(p, stream);
+      }
       // Pair causal key blocks when the grid outnumbers the resident workgroups.
       const int npairs = p.batch * p.kv_heads;
       const int resident = resident_workgroups(Occupancy<T, D>::value);

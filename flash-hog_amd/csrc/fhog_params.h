@@ -69,6 +69,10 @@ hipError_t launch_bwdbwd_stage1_fused(const BwdBwdParams<T>& p, hipStream_t s);
 // launch_bwdbwd selects it.
 template <typename T, bool CAUSAL>
 hipError_t launch_bwdbwd_stage1_q32(const BwdBwdParams<T>& p, hipStream_t s);
+// Stage 2 with 32 keys per wave at one wave per SIMD (bf16, D = 64);
+// launch_bwdbwd selects it.
+template <bool CAUSAL>
+hipError_t launch_bwdbwd_stage2_k32(const BwdBwdParams<__bf16>& p, hipStream_t s);
 // Stage 2 with 16 keys per wave (2-byte types, D = 128); launch_bwdbwd selects it.
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd_stage2_k16(const BwdBwdParams<T>& p, hipStream_t s);
