@@ -577,7 +577,11 @@ def main(argv=None):
                      "alg_flops_per_launch": s1_alg, "ms_per_launch": round(s1_ms, 5)},
         "cpu_baseline": None if cpu is None else {k: (round(v, 6) if isinstance(v, float) else v)
                                                   for k, v in cpu.items()},
-        "detail": {"stage2_ms": round(s2_ms, 5), "executed_mfma_tflops": round(exec_tflops, 3),
+        # whole step: 24 d flops per unmasked pair over the whole double
+        # backward's time (the roofline entry above credits stage 1 with the
+        # score products stage 2 recomputes)
+        "detail": {"whole_step_frac": round(value / MI355X_PEAK_BF16_TFLOPS, 5),
+                   "stage2_ms": round(s2_ms, 5), "executed_mfma_tflops": round(exec_tflops, 3),
                    "alg_gflop_per_step": round(alg_flops / 1e9, 3), "peak_extra_hbm_bytes": int(peak_extra),
                    "hvp_ms": round(hvp_ms, 5), "wall_ms_per_step": round(wall * 1e3 / args.steps, 5)},
     }
