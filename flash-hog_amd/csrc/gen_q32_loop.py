@@ -31,6 +31,14 @@ next step needs. Each step begins by waiting for tile t + 1's LDS DMA,
 the workgroup barrier and the DMA of tile t + 6 into the stage tile t - 2
 left (an 8-stage ring).
 
+Tile numbers are ring positions: the block's key tile j is ring tile t0 + j
+(operand t0, less than 8), in stage (t0 + j) mod 8, and the operands nkt,
+nfull, hi0 and rag count in those numbers (t0 + the block's tile count, and so
+on; rag stays 0xffffffff without a ragged tail), klb in keys (its value plus
+32 t0). A workgroup that sweeps several blocks starts each one where the
+previous one left the ring, so it can issue the next block's first tiles
+while waves still read the last stages of the current one.
+
 Hazards. The statement is opaque to the compiler's hazard recognizer, so
 the generated code keeps the distances the compiler itself inserts for
 v_mfma_f32_32x32x16 on gfx950 (measured by compiling the patterns): a matrix
@@ -522,7 +530,7 @@ class Gen:
         self.emit(f"s_mov_b64 s[{SG['gptr']}:{SG['gptr'] + 1}], %[gptr]")
         self.emit(f"s_mov_b64 s[{SG['gstep']}:{SG['gstep'] + 1}], %[gstep]")
         self.emit(f"s_mov_b32 s{SG['hi']}, %[hi0]")
-        self.emit(f"s_mov_b32 s{SG['t']}, 0")
+        self.emit(f"s_mov_b32 s{SG['t']}, %[t0]")
         self.advance(0, "pro")
         for x in self.addr_row_ops(0, SG["k2"]):
             self.emit(x)
@@ -627,16 +635,17 @@ class Gen:
         out = self.out
         L = self.lbl
         self.block_prologue()
-        self.emit(f"s_cmp_eq_u32 %[nkt], 1")
+        self.emit(f"s_add_u32 s{SG['k0']}, s{SG['t']}, 1")
+        self.emit(f"s_cmp_eq_u32 %[nkt], s{SG['k0']}")
         self.emit(f"s_cbranch_scc1 {L('single_sel')}")
-        self.emit(f"s_cmp_eq_u32 %[nfull], 0")
+        self.emit(f"s_cmp_eq_u32 %[nfull], s{SG['t']}")
         self.emit(f"s_cbranch_scc1 {L('first_m')}")
         self.block_first(masked=False)
-        self.emit(f"s_mov_b32 s{SG['t']}, 1")
+        self.emit(f"s_add_u32 s{SG['t']}, s{SG['t']}, 1")
         self.emit(f"s_branch {L('loop')}")
         self.emit(f"{L('first_m')}:")
         self.block_first(masked=True)
-        self.emit(f"s_mov_b32 s{SG['t']}, 1")
+        self.emit(f"s_add_u32 s{SG['t']}, s{SG['t']}, 1")
         self.emit(f"{L('loop')}:")
         self.emit(f"s_add_u32 s{SG['k0']}, s{SG['t']}, 1")
         self.emit(f"s_cmp_ge_u32 s{SG['k0']}, %[nkt]")
@@ -663,7 +672,7 @@ class Gen:
         self.block_last(masked=True)
         self.emit(f"s_branch {L('end')}")
         self.emit(f"{L('single_sel')}:")
-        self.emit(f"s_cmp_eq_u32 %[nfull], 0")
+        self.emit(f"s_cmp_eq_u32 %[nfull], s{SG['t']}")
         self.emit(f"s_cbranch_scc1 {L('single_m')}")
         self.block_last(masked=False, single=True)
         self.emit(f"s_branch {L('end')}")

@@ -7,8 +7,8 @@ combination, treating vector, LDS and matrix instructions as no-ops, and
 checks:
   - the sweep ends, after exactly one LDS DMA of every tile the kernel's own
     prologue did not issue, in order, from that tile's global address and
-    into ring stage (tile mod 8), with the ragged tail's offsets only for
-    the ragged tile;
+    into ring stage ((t0 + tile) mod 8) for the block's first ring tile t0,
+    with the ragged tail's offsets only for the ragged tile;
   - at each DMA the tile it overwrites (tile - 8) was last read in a step
     that every wave has finished (its step index is at least two less than
     the current one), and every tile a step reads has been waited for;
@@ -148,12 +148,13 @@ LDS_KV, LDS_W, GBASE, GSTEP = 0x10000, 0x10000 + 3 * 4096, 1 << 40, 32 * 2048
 def test_sweep_control_flow(variant):
     _, dtype, pre = variant
     prog = program(dtype, pre)
-    for nkt in range(1, 24):
+    for nkt, t0 in [(k, 0) for k in range(1, 24)] + [(k, t) for k in (1, 2, 5, 6, 7, 9, 14) for t in (3, 7)]:
         for nfull in sorted({0, 1, nkt // 2, nkt - 1, nkt}):
             for ragged in (False, True):
                 hi0 = min(4, nkt - 1)
-                rag = nkt - 1 if ragged else 0xFFFFFFFF
-                ops = dict(nkt=nkt, nfull=nfull, rag=rag, hi0=hi0, ldskv=LDS_KV, ldsw=LDS_W,
+                rag = t0 + nkt - 1 if ragged else 0xFFFFFFFF
+                # operands in ring-tile numbers: the block's tile j is ring tile t0 + j
+                ops = dict(nkt=t0 + nkt, nfull=t0 + nfull, rag=rag, hi0=t0 + hi0, t0=t0, ldskv=LDS_KV, ldsw=LDS_W,
                            gptr=GBASE + (hi0 + 1) * GSTEP, gstep=GSTEP)
                 # the 64-bit operands are moved with s_mov_b64 from these values
                 ev = run(prog, ops)
@@ -165,7 +166,7 @@ def test_sweep_control_flow(variant):
                     for j in range(4):
                         _, gptr, m0, which = dmas[4 * i + j]
                         assert gptr == GBASE + kt * GSTEP, (nkt, kt, gptr)
-                        assert m0 == LDS_W + (kt % 8) * 4 * 4096 + 1024 * j, (nkt, kt, m0)
+                        assert m0 == LDS_W + ((t0 + kt) % 8) * 4 * 4096 + 1024 * j, (nkt, t0, kt, m0)
                         want = "%[vp{}]".format(j) if (ragged and kt == nkt - 1) else "%[vo{}]".format(j)
                         assert which == want.replace("%", "%"), (nkt, kt, which)
                 # Ring discipline: number the barriers; the DMA of tile kt may
@@ -272,7 +273,8 @@ def test_sweep_hazards(variant):
     prog = program(dtype, pre)
     for nkt, nfull in ((1, 0), (1, 1), (2, 0), (2, 2), (3, 1), (7, 4), (12, 12), (12, 8)):
         hi0 = min(4, nkt - 1)
-        ops = dict(nkt=nkt, nfull=nfull, rag=0xFFFFFFFF, hi0=hi0, ldskv=LDS_KV, ldsw=LDS_W,
+        t0 = nkt % 8
+        ops = dict(nkt=t0 + nkt, nfull=t0 + nfull, rag=0xFFFFFFFF, hi0=t0 + hi0, t0=t0, ldskv=LDS_KV, ldsw=LDS_W,
                    gptr=GBASE + (hi0 + 1) * GSTEP, gstep=GSTEP)
         trace = []
         run(prog, ops, trace=trace)
