@@ -90,7 +90,7 @@ def make_inputs(torch, B, N, H, D, dtype, device, seed=0):
 # of this benchmark (FETCH_SIZE, then WRITE_SIZE) and calibrated with the same
 # counters on a plain device copy of known size; written by the profiling step
 # into profiles/ (see the file for the commands).
-TRAFFIC_FILE = REPO / "profiles" / "bwdbwd_q_fused_kernel_b4_n2048_h16_d64_bf16_causal.traffic.json"
+TRAFFIC_FILE = REPO / "profiles" / "bwdbwd_q32_kernel_b4_n2048_h16_d64_bf16_causal.traffic.json"
 
 
 def stage1_traffic():
@@ -517,8 +517,9 @@ def main(argv=None):
     s1_alg = 18.0 * D * pairs
     s1_tflops = s1_alg / (s1_ms * 1e-3) / 1e12
     # executed MFMA work per unmasked pair: stage 1 = 11 products (5 score and
-    # 6 output products in one sweep), stage 2 = 8 products; 2 * d flops each
-    exec_tflops = (22.0 + 16.0) * D * pairs / (ms_per_step * 1e-3) / 1e12
+    # 6 output products in one sweep, 22 d flops) and 1 d for a product with a
+    # ones operand that sums x over the keys, stage 2 = 8 products (16 d)
+    exec_tflops = (23.0 + 16.0) * D * pairs / (ms_per_step * 1e-3) / 1e12
     traffic = stage1_traffic()
 
     # Peak memory of one call with torch-owned outputs, against the inputs.
@@ -569,7 +570,7 @@ def main(argv=None):
         "config": {"workload": "attention double backward (Flash-HOG), causal", "batch": B, "seq_len": N,
                    "heads": H, "head_dim": D, "scale": scale, "parallelism": "none (1 GPU)"},
         "pct_of_bf16_peak": round(100.0 * value / MI355X_PEAK_BF16_TFLOPS, 3),
-        "roofline": {"bound": "mfma", "kernel": "bwdbwd_q_fused_kernel (stage 1, passes 1-3 in one sweep)",
+        "roofline": {"bound": "mfma", "kernel": "bwdbwd_q32_kernel (stage 1, passes 1-3 in one sweep)",
                      "achieved": round(s1_tflops, 3), "peak": MI355X_PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(s1_tflops / MI355X_PEAK_BF16_TFLOPS, 5),
                      "traffic": None if traffic is None else traffic["bytes"],

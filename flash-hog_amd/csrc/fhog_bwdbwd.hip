@@ -636,15 +636,17 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
 
 }  // namespace
 
-// Stage 1 for 2-byte types at D = 64 runs the fused kernel (16 queries per
-// wave, two waves per SIMD) unless FLASH_HOG_STAGE1=q32 selects the kernel
-// with 32 queries per wave at one wave per SIMD and a hand-scheduled sweep
-// (fhog_bwdbwd_q32.hip). Both give the same results to rounding; at
-// B4 N2048 H16 D64 causal bf16 the fused kernel is about 4 % faster. Read at
-// every launch, so a process can switch between them.
-inline bool stage1_q32_selected() {
+// Stage 1 for 2-byte types at D = 64 runs the kernel with 32 queries per
+// wave at one wave per SIMD, a hand-scheduled sweep and a persistent grid
+// (fhog_bwdbwd_q32.hip) unless FLASH_HOG_STAGE1=fused selects the fused
+// kernel (16 queries per wave, two waves per SIMD), which serves D = 128 and
+// 256. Both give the same results to rounding; the q32 kernel is 3-6 % faster
+// on every D = 64 configuration measured (179 against 185 us at B4 N2048 H16
+// causal bf16, 137 against 146 us at B8 N1000 H12 fp16). Read at every launch,
+// so a process can switch between them.
+inline bool stage1_fused_selected() {
   const char* v = std::getenv("FLASH_HOG_STAGE1");
-  return v != nullptr && std::strcmp(v, "q32") == 0;
+  return v != nullptr && std::strcmp(v, "fused") == 0;
 }
 
 // Stage 2 for bf16 at D = 64 runs bwdbwd_k_kernel below (32 keys per wave,
@@ -664,8 +666,8 @@ hipError_t launch_bwdbwd(const BwdBwdParams<T>& p, hipStream_t stream, int stage
   if (stages & 1) {
     hipError_t e;
     if constexpr (sizeof(T) == 2 && D == 64) {
-      e = stage1_q32_selected() ? launch_bwdbwd_stage1_q32<T, CAUSAL>(p, stream)
-                                : launch_bwdbwd_stage1_fused<T, D, CAUSAL>(p, stream);
+      e = stage1_fused_selected() ? launch_bwdbwd_stage1_fused<T, D, CAUSAL>(p, stream)
+                                  : launch_bwdbwd_stage1_q32<T, CAUSAL>(p, stream);
     } else if constexpr (sizeof(T) == 2) {
       e = launch_bwdbwd_stage1_fused<T, D, CAUSAL>(p, stream);
     } else {

@@ -1,6 +1,7 @@
 // Stage 1 of the Flash-HOG double backward (passes 1-3) in one sweep over the
-// keys, for 2-byte types at D = 64, 128 and 256 (fhog_bwdbwd.hip holds the
-// two-sweep stage 1 used for fp32, and stage 2). The math follows
+// keys, for 2-byte types at D = 128 and 256, and at D = 64 when
+// FLASH_HOG_STAGE1=fused selects it over fhog_bwdbwd_q32.hip (fhog_bwdbwd.hip
+// holds the two-sweep stage 1 used for fp32, and stage 2). The math follows
 // flash_hog/_jax_refs/jax_impl.py:273-336 and the pass split of
 // flash_hog/jax/_pallas_gpu_kernel.py:149-278; outputs and row statistics are
 // those of fhog_bwdbwd.hip's stage 1.

@@ -1,12 +1,13 @@
-"""The second stage-1 kernel for 2-byte types at D = 64 (fhog_bwdbwd_q32.hip:
-32 queries per wave at one wave per SIMD, hand-scheduled sweep), which
-FLASH_HOG_STAGE1=q32 selects at launch.
+"""The fused stage-1 kernel at D = 64 for 2-byte types
+(fhog_bwdbwd_fused.hip: 16 queries per wave, two waves per SIMD), which
+FLASH_HOG_STAGE1=fused selects at launch in place of the default 32-query
+kernel (fhog_bwdbwd_q32.hip) that every other D = 64 test runs.
 
 Every D = 64 2-byte case of the parity, scale, single-key and random-sweep
 suites runs again with it selected, against the fp64 oracle and at the same
-tolerances; the standard and ragged full-size configurations compare its
-outputs with the fused kernel's on the same inputs. Its control flow and
-hazard distances are checked on the CPU (tests/test_q32_loop_control.py).
+tolerances; the standard and ragged full-size configurations compare the two
+kernels' outputs on the same inputs. The q32 kernel's control flow and hazard
+distances are checked on the CPU (tests/test_q32_loop_control.py).
 """
 
 from __future__ import annotations
@@ -24,8 +25,8 @@ TWO_BYTE = (torch.bfloat16, torch.float16)
 
 
 @pytest.fixture
-def q32(monkeypatch):
-    monkeypatch.setenv("FLASH_HOG_STAGE1", "q32")
+def fused(monkeypatch):
+    monkeypatch.setenv("FLASH_HOG_STAGE1", "fused")
 
 
 def _d64(cases, dim, dtype):
@@ -39,22 +40,22 @@ PROBLEMS = _d64(sweep.PROBLEMS, 6, 7)
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_q32_bwdbwd_matches_oracle(case, cuda_device, q32):
+def test_fused_d64_bwdbwd_matches_oracle(case, cuda_device, fused):
     parity.test_bwdbwd_matches_oracle(case, cuda_device)
 
 
 @pytest.mark.parametrize("case", SCALE_CASES, ids=[c[0] for c in SCALE_CASES])
-def test_q32_other_scales(case, cuda_device, q32):
+def test_fused_d64_other_scales(case, cuda_device, fused):
     parity.test_all_kernels_other_scales(case, cuda_device)
 
 
 @pytest.mark.parametrize("case", SINGLE_KEY_CASES, ids=[c[0] for c in SINGLE_KEY_CASES])
-def test_q32_single_key_rows_are_exact(case, cuda_device, q32):
+def test_fused_d64_single_key_rows_are_exact(case, cuda_device, fused):
     parity.test_single_key_rows_are_exact(case, cuda_device)
 
 
 @pytest.mark.parametrize("problem", PROBLEMS, ids=[p[0] for p in PROBLEMS])
-def test_q32_random_problem(problem, cuda_device, q32):
+def test_fused_d64_random_problem(problem, cuda_device, fused):
     sweep.test_random_problem_all_kernels(problem, cuda_device)
 
 
