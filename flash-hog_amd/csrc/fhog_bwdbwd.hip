@@ -530,6 +530,17 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
           issue(i + NST - 1, nxt);
           advance(nxt);
         }
+        // Tile i + 1's statistics are read after the next barrier. With a ring
+        // of three or more stages their DMA went out two or more iterations
+        // ago, and they are finished here, before this tile's work, so that
+        // the LDS round trip overlaps wave 3's own products instead of
+        // delaying the barrier; with two stages, after this tile's work.
+        if constexpr (NST >= 3) {
+          if (wave == 3 && i + 1 < total) {
+            wait_stats(i + 1);
+            finish_stats(i + 1);
+          }
+        }
         const int q0 = (qt_begin + cur.qt) * BQ;
         const bool active = k0 < p.nk && (!CAUSAL || q0 + BQ - 1 >= k0 - p.coff);
         if (active) {
@@ -603,10 +614,11 @@ bwdbwd_k_kernel(BwdBwdParams<T> p, int pairs, int chunk) {
             }
           }
         }
-        // Tile i + 1's statistics are read after the next barrier.
-        if (wave == 3 && i + 1 < total) {
-          wait_stats(i + 1);
-          finish_stats(i + 1);
+        if constexpr (NST < 3) {
+          if (wave == 3 && i + 1 < total) {
+            wait_stats(i + 1);
+            finish_stats(i + 1);
+          }
         }
       }
     }
