@@ -348,6 +348,8 @@ def run_configs(args):
     log("| config | ms | alg. TFLOP/s | % bf16 peak | stage 1 ms | stage 2 ms | peak extra HBM | one fp32 N x N tensor |")
     log("|---|--:|--:|--:|--:|--:|--:|--:|")
     for c in CONFIGS:
+        if args.config and not any(sel in c["name"] for sel in args.config):
+            continue
         B, N, H, D = c["batch"], c["seq"], c["heads"], c["head_dim"]
         dtype, causal = dtypes[c["dtype"]], c["causal"]
         scale = 1.0 / math.sqrt(D)
@@ -423,6 +425,8 @@ def main(argv=None):
                     help="run one device copy of this many MiB first (PMC byte-counter calibration)")
     ap.add_argument("--configs", action="store_true",
                     help="time the double backward on every GPU configuration of the benchmark set instead")
+    ap.add_argument("--config", action="append", default=[],
+                    help="with --configs: only configurations whose name contains this text (repeatable)")
     ap.add_argument("--hvp-table", choices=sorted(HVP_TABLES),
                     help="time the end-to-end HVP on the shapes of one of the reference's HVP tables instead")
     args = ap.parse_args(argv)
