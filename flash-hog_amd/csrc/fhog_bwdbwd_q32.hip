@@ -224,10 +224,10 @@ bwdbwd_q32_kernel(BwdBwdParams<T> p, int nitems) {
     // compiler 67 vector registers for everything alive across it).
     int lane_b = lane;
     asm volatile("" : "+v"(n), "+v"(g), "+v"(lane_b));
-    // The sweep's LDS read offsets, likewise rebuilt per block. The
-    // transposed reads' second address is the first with bit 4 flipped
-    // (SwzFrags::trf); ring stages are 32-byte aligned, so the flip can be
-    // applied to the per-lane offset.
+    // The sweep's LDS read offsets and its DMAs' per-lane source offsets,
+    // likewise rebuilt per block. The transposed reads' second address is
+    // the first with bit 4 flipped (SwzFrags::trf); ring stages are 32-byte
+    // aligned, so the flip can be applied to the per-lane offset.
     SwzFrags<T, D> fr;
     fr.init(lane_b);
     dma.init(row_bytes, BK, lane_b);
