@@ -16,6 +16,9 @@
 // in kernel 1 (row statistics are per-lane scalars), direct in kernel 2,
 // whose score accumulators start at the per-query constants -L / scale and -D
 // so that the MFMAs fold them in.
+#include <cstdlib>
+#include <cstring>
+
 #include "fhog_device.h"
 #include "fhog_params.h"
 
@@ -424,6 +427,16 @@ bwd_k_kernel(BwdParams<T> p, int chunk) {
 
 }  // namespace
 
+// The dK/dV kernel for 2-byte types at D = 64: the kernel with 64 keys per
+// wave and a generated sweep (fhog_bwd_k64.hip) unless FLASH_HOG_BWD=compiled
+// selects bwd_k_kernel above. Both give the same results to rounding; at
+// B4 N2048 H16 D64 causal bf16 the first backward takes 142 against 149 us
+// with the compiled kernel. Read at every launch.
+inline bool bwd_k64_selected() {
+  const char* v = std::getenv("FLASH_HOG_BWD");
+  return v == nullptr || std::strcmp(v, "compiled") != 0;
+}
+
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t stream) {
   const int nqb = (p.nq + 32 * kWaves - 1) / (32 * kWaves);
@@ -434,6 +447,9 @@ hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t stream) {
                      grid_chunk(nq_pairs, nqb, resident));
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if constexpr (sizeof(T) == 2 && D == 64) {
+    if (bwd_k64_selected()) return launch_bwd_k64<T, CAUSAL>(p, stream);
+  }
   hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL, 0>), dim3(nkb * nk_pairs), dim3(kThreads), 0, stream, p,
                      grid_chunk(nk_pairs, nkb, resident));
   if constexpr (KSplit<T, D>::value) {
