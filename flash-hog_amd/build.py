@@ -56,6 +56,7 @@ SOURCE_FLAGS: dict[str, list[str]] = {
     "fhog_bwdbwd_q32.hip": _MAX_ILP,
     "fhog_bwdbwd_k32.hip": _MAX_ILP,
     "fhog_bwd_k64.hip": _MAX_ILP,
+    "fhog_bwd_q64.hip": _MAX_ILP,
     "fhog_bwdbwd.hip": _MAX_ILP,
     "fhog_bwdbwd_k16.hip": _MAX_ILP,
     "fhog_fwd.hip": _MAX_ILP,

@@ -90,8 +90,12 @@ bwd_q_kernel(BwdParams<T> p, int chunk) {
       qf[ks] = *reinterpret_cast<const V8<T>*>(p.q + off);
       dof[ks] = *reinterpret_cast<const V8<T>*>(p.dout + off);
       const V8<T> of = *reinterpret_cast<const V8<T>*>(p.o + off);
+      if constexpr (sizeof(T) == 2) {
+        dpart = dot8<T>(of, dof[ks], dpart);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dpart += (float)of[e] * (float)dof[ks][e];
+        for (int e = 0; e < 8; ++e) dpart += (float)of[e] * (float)dof[ks][e];
+      }
     } else {
       qf[ks] = zero8<T>();
       dof[ks] = zero8<T>();
@@ -427,14 +431,29 @@ bwd_k_kernel(BwdParams<T> p, int chunk) {
 
 }  // namespace
 
-// The dK/dV kernel for 2-byte types at D = 64: the kernel with 64 keys per
-// wave and a generated sweep (fhog_bwd_k64.hip) unless FLASH_HOG_BWD=compiled
-// selects bwd_k_kernel above. Both give the same results to rounding; at
-// B4 N2048 H16 D64 causal bf16 the first backward takes 142 against 149 us
-// with the compiled kernel. Read at every launch.
-inline bool bwd_k64_selected() {
-  const char* v = std::getenv("FLASH_HOG_BWD");
-  return v == nullptr || std::strcmp(v, "compiled") != 0;
+// The first backward for 2-byte types at D = 64 has two kernels for each
+// half of its work: dK/dV in bwd_k_kernel above or in bwd_k64_kernel
+// (fhog_bwd_k64.hip: 64 keys per wave at one wave per SIMD, generated sweep),
+// dQ in bwd_q_kernel above or in bwd_q64_kernel (fhog_bwd_q64.hip, the same
+// with 64 queries per wave). A one-wave kernel runs one 256-row block per CU
+// at a time and gains nothing when a CU is left alone, so it is taken when
+// its grid fills whole rounds of the resident workgroups (or at least six),
+// and the compiled kernel, whose second workgroup per CU runs faster alone,
+// otherwise: first backward at B4 N2048 H16 causal bf16 138.7-140.7 us with
+// both one-wave kernels against 148.5-149.1 with both compiled ones, while
+// at B8 N2048 H12 causal (1.5 rounds) the one-wave dQ kernel took 258
+// against 241 us. FLASH_HOG_BWD (dK/dV) and FLASH_HOG_BWDQ (dQ) = compiled or
+// k64 / q64 force a kernel; read at every launch.
+inline bool one_wave_grid(int workgroups, int resident) {
+  return resident > 0 && workgroups > 0 && (workgroups % resident == 0 || workgroups >= 6 * resident);
+}
+inline bool one_wave_selected(const char* var, const char* name, int nb, int npairs, bool causal) {
+  const char* v = std::getenv(var);
+  if (v != nullptr && std::strcmp(v, name) == 0) return true;
+  if (v != nullptr && std::strcmp(v, "compiled") == 0) return false;
+  const int resident = resident_workgroups(1);
+  const int pairs = block_pairing(causal, nb, npairs, resident, 1);
+  return one_wave_grid((pairs ? (nb + 1) / 2 : nb) * npairs, resident);
 }
 
 template <typename T, int D, bool CAUSAL>
@@ -443,12 +462,22 @@ hipError_t launch_bwd(const BwdParams<T>& p, hipStream_t stream) {
   const int nkb = (p.nk + 32 * kWaves - 1) / (32 * kWaves);
   const int resident = resident_workgroups(Occupancy<T, D>::value);
   const int nq_pairs = p.batch * p.heads, nk_pairs = p.batch * p.kv_heads;
-  hipLaunchKernelGGL((bwd_q_kernel<T, D, CAUSAL>), dim3(nqb * nq_pairs), dim3(kThreads), 0, stream, p,
-                     grid_chunk(nq_pairs, nqb, resident));
-  hipError_t e = hipGetLastError();
+  hipError_t e = hipSuccess;
+  if constexpr (sizeof(T) == 2 && D == 64) {
+    if (one_wave_selected("FLASH_HOG_BWDQ", "q64", (p.nq + 255) / 256, nq_pairs, CAUSAL))
+      e = launch_bwd_q64<T, CAUSAL>(p, stream);
+    else
+      hipLaunchKernelGGL((bwd_q_kernel<T, D, CAUSAL>), dim3(nqb * nq_pairs), dim3(kThreads), 0, stream, p,
+                         grid_chunk(nq_pairs, nqb, resident));
+  } else {
+    hipLaunchKernelGGL((bwd_q_kernel<T, D, CAUSAL>), dim3(nqb * nq_pairs), dim3(kThreads), 0, stream, p,
+                       grid_chunk(nq_pairs, nqb, resident));
+  }
+  if (e == hipSuccess) e = hipGetLastError();
   if (e != hipSuccess) return e;
   if constexpr (sizeof(T) == 2 && D == 64) {
-    if (bwd_k64_selected()) return launch_bwd_k64<T, CAUSAL>(p, stream);
+    if (one_wave_selected("FLASH_HOG_BWD", "k64", (p.nk + 255) / 256, nk_pairs, CAUSAL))
+      return launch_bwd_k64<T, CAUSAL>(p, stream);
   }
   hipLaunchKernelGGL((bwd_k_kernel<T, D, CAUSAL, 0>), dim3(nkb * nk_pairs), dim3(kThreads), 0, stream, p,
                      grid_chunk(nk_pairs, nkb, resident));

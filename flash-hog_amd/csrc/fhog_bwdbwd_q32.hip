@@ -56,21 +56,6 @@ __device__ __forceinline__ const void* uni(const void* x) {
   return (const void*)(uintptr_t)((uint64_t)uni((uint32_t)u) | ((uint64_t)uni((uint32_t)(u >> 32)) << 32));
 }
 
-// acc + <a, b> over eight 2-byte elements, two products per instruction.
-template <typename T> __device__ __forceinline__ float dot8(V8<T> a, V8<T> b, float acc) {
-  typedef T T2 __attribute__((ext_vector_type(2)));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const T2 x = {a[2 * i], a[2 * i + 1]};
-    const T2 y = {b[2 * i], b[2 * i + 1]};
-    if constexpr (std::is_same_v<T, __bf16>)
-      acc = __builtin_amdgcn_fdot2_f32_bf16(x, y, acc, false);
-    else
-      acc = __builtin_amdgcn_fdot2(x, y, acc, false);
-  }
-  return acc;
-}
-
 // A workgroup's share of the grid. The grid is persistent (at most one
 // workgroup per CU, the most that fit at one wave per SIMD) and walks a list
 // of items: with a causal mask item r of a (batch, head) pair is the query

@@ -103,6 +103,25 @@ __device__ __forceinline__ float xgroup_max(float x) { return fmaxf(x, __shfl_xo
 // Row index (within a 32-row C tile) held by register r of a lane in group g.
 __device__ __forceinline__ int crow(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 
+// acc + <a, b> over eight 2-byte elements, two products per v_dot2, pairs in
+// order. The first backward's two dQ kernels form D = rowsum(O dO) with it,
+// so that D does not depend on which of them runs (left to itself the
+// compiler turns such a sum into v_dot2 in one kernel and into mixed-precision
+// fmas in another, which round differently).
+template <typename T> __device__ __forceinline__ float dot8(V8<T> a, V8<T> b, float acc) {
+  typedef T T2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const T2 x = {a[2 * i], a[2 * i + 1]};
+    const T2 y = {b[2 * i], b[2 * i + 1]};
+    if constexpr (std::is_same_v<T, __bf16>)
+      acc = __builtin_amdgcn_fdot2_f32_bf16(x, y, acc, false);
+    else
+      acc = __builtin_amdgcn_fdot2(x, y, acc, false);
+  }
+  return acc;
+}
+
 // ---------------------------------------------------------------------------
 // Swizzled tiles written straight from global memory into LDS.
 //

@@ -74,9 +74,13 @@ hipError_t launch_bwdbwd_stage1_q32(const BwdBwdParams<T>& p, hipStream_t s);
 template <bool CAUSAL>
 hipError_t launch_bwdbwd_stage2_k32(const BwdBwdParams<__bf16>& p, hipStream_t s);
 // The first backward's dK/dV kernel with 64 keys per wave at one wave per SIMD
-// (2-byte types, D = 64); launch_bwd selects it unless FLASH_HOG_BWD=compiled.
+// (2-byte types, D = 64); launch_bwd selects it for grids of whole rounds.
 template <typename T, bool CAUSAL>
 hipError_t launch_bwd_k64(const BwdParams<T>& p, hipStream_t s);
+// The first backward's dQ kernel with 64 queries per wave at one wave per SIMD
+// (2-byte types, D = 64); launch_bwd selects it for grids of whole rounds.
+template <typename T, bool CAUSAL>
+hipError_t launch_bwd_q64(const BwdParams<T>& p, hipStream_t s);
 // Stage 2 with 16 keys per wave (2-byte types, D = 128); launch_bwdbwd selects it.
 template <typename T, int D, bool CAUSAL>
 hipError_t launch_bwdbwd_stage2_k16(const BwdBwdParams<T>& p, hipStream_t s);

@@ -302,9 +302,17 @@ def _ws(ins):
 CHAIN = 5
 
 
+# bf16 operands of the output products (P, dS): each value written is read by
+# exactly two matrix instructions (column blocks dt = 0, 1) before the next
+# write, so no conversion overwrites a tile's values before its output
+# products have taken them
+OUT_OPERANDS = {("v", r) for r in [b[h] + i for b in (G.EDS, G.EP) for h in range(2) for i in range(8)]}
+
+
 def check_hazards(trace):
     last_mfma_write, last_valu_write, last_trans_write = {}, {}, {}
     chain = {}  # register -> matrix products in its current chain
+    reads = {}  # output operand register -> matrix reads of its current value
     lds_pending = []
     clock = 0
     for ins in trace:
@@ -330,6 +338,9 @@ def check_hazards(trace):
             for r in _regs(c):
                 if r in last_valu_write:
                     assert last_valu_write[r] < last_mfma_write.get(r, -1), f"accumulator overwritten before {ins}"
+            for r in (_regs(a) | _regs(b)) & OUT_OPERANDS:
+                reads[r] = reads.get(r, 0) + 1
+                assert reads[r] <= 2, f"{ins} reads an output operand a third time"
             for r in _regs(dst):
                 last_mfma_write[r] = clock
                 chain[r] = 1 if c == "0" else chain.get(r, 0) + 1
@@ -349,6 +360,9 @@ def check_hazards(trace):
                     assert clock - last_trans_write[r] >= 2, f"transcendental result read by {ins} too early"
             for regs in lds_pending:
                 assert not (regs & (srcs | _regs(dst))), f"vector instruction touches a pending LDS read: {ins}"
+            for r in _regs(dst) & OUT_OPERANDS:
+                assert reads.get(r, 2) == 2, f"{ins} overwrites an output operand read {reads.get(r)} times"
+                reads[r] = 0
             for r in _regs(dst):
                 last_valu_write[r] = clock
                 if op == "v_exp_f32":
