@@ -101,6 +101,29 @@ def frag(k):
     return f"a[{FRAG0 + 4 * k}:{FRAG0 + 4 * k + 3}]"
 
 
+def issue_cost(x):
+    """Approximate issue cycles of an instruction at one wave per SIMD, as
+    measured by looping instruction mixes: a wave-wide vector instruction
+    about 5 (an exponential about 8.6), an LDS DMA about 10, s_nop n n + 1,
+    a scalar instruction 1-4 (more in dependent chains). LDS reads are paced
+    separately and waits and barriers cost what they wait for; both count 0.
+    A matrix instruction leaves about 32 cycles for the others."""
+    op = x.split()[0]
+    if op.startswith("ds_read") or op in ("s_waitcnt", "s_barrier") or op.endswith(":"):
+        return 0.0
+    if op == "v_exp_f32":
+        return 8.6
+    if op.startswith("v_"):
+        return 5.2
+    if op.startswith("global_load"):
+        return 10.0
+    if op == "s_nop":
+        return int(x.split()[1]) + 1.0
+    if op.startswith("s_"):
+        return 2.0
+    return 0.0
+
+
 class Frag:
     """An MFMA A operand read from LDS into fragment slot `slot`: one
     ds_read_b128 (row fragment) or two ds_read_b64_tr_b16 (transposed)."""
@@ -430,10 +453,13 @@ class Gen:
 
     # ----- phases -----
     def phase(self, sch, mfmas, valu, side=None):
-        """Issues mfmas with the vector ops spread evenly between them and LDS
-        reads paced by the scheduler. side maps a matrix instruction's index
-        in this phase (-1: before the first) to instructions emitted right
-        after it."""
+        """Issues mfmas with the vector ops between them and LDS reads paced
+        by the scheduler. side maps a matrix instruction's index in this phase
+        (-1: before the first) to instructions emitted right after it. The
+        vector ops keep their order and fill the gaps so that each gap's
+        issue cost (issue_cost: its side instructions and vector ops) is about
+        the phase's average: a gap that holds the DMAs or an address chain
+        takes fewer vector ops."""
         side = side or {}
         groups = [list(op) if isinstance(op, tuple) else [op] for op in valu]
         for x in side.get(-1, []):
@@ -450,11 +476,20 @@ class Gen:
             return
         sch.issue_reads()
         gi = 0
+        gcost = [sum(issue_cost(x) for x in g) for g in groups]
+        scost = [sum(issue_cost(x) for x in side.get(i, [])) for i in range(n)]
+        placed = sum(issue_cost(x) for x in side.get(-1, []))  # falls in the first gap
+        total = placed + sum(gcost) + sum(scost)
         for i, (text, frags) in enumerate(mfmas):
             sch.mfma(text, frags)
             for x in side.get(i, []):
                 sch.emit(x)
-            target = ((i + 1) * len(groups)) // n
+            placed += scost[i]
+            goal = (i + 1) * total / n
+            target = gi
+            while target < len(groups) and (i == n - 1 or placed + gcost[target] / 2 <= goal):
+                placed += gcost[target]
+                target += 1
             half = (gi + target) // 2
             while gi < half:
                 for x in groups[gi]:
@@ -597,8 +632,11 @@ class Gen:
         self.phase(sch, mf_o, self.e1(masked), side_a)
         # every read through the old transposed addresses has been issued
         assert all(e[0] not in self.rest_tr(tf) for e in sch.queue)
-        side_b = {-1: self.addr_tr_ops(0, SG["k1"])}
-        self.next_step_frags(sch, n_blk, len(mf_o))
+        # tile t's transposed addresses after the first score product (the gap
+        # before it holds phase A's last vector ops); the next step's reads
+        # through them are queued from there on
+        side_b = {0: self.addr_tr_ops(0, SG["k1"])}
+        self.next_step_frags(sch, n_blk, len(mf_o) + 1)
         self.phase(sch, mf_s, self.e2(), side_b)
         self.end_with_prefetch(sch)
         self.emit(f"s_add_u32 s{SG['t']}, s{SG['t']}, 1")
