@@ -337,7 +337,7 @@ class BQ64:
             for x in side.get(i, []):
                 put_side(x)
             ops = slots.get(i, [])
-            h = len(ops) // 2
+            h = 0  # the gap's LDS reads before its vector ops
             for op in ops[:h]:
                 put(op)
             sch.issue_reads()

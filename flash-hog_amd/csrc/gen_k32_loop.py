@@ -426,7 +426,7 @@ class K32:
             for x in side.get(i, []):
                 sch.emit(x)
             ops = slots.get(i, [])
-            h = len(ops) // 2
+            h = 0  # the gap's LDS reads before its vector ops
             for op in ops[:h]:
                 put(op)
             sch.issue_reads()
@@ -579,7 +579,7 @@ class K32:
                     else:
                         sch.emit(x)
                 ops = slots.get(i, [])
-                h = len(ops) // 2
+                h = 0  # the gap's LDS reads before its vector ops
                 for op in ops[:h]:
                     put(op)
                 sch.issue_reads()

@@ -490,11 +490,8 @@ class Gen:
             while target < len(groups) and (i == n - 1 or placed + gcost[target] / 2 <= goal):
                 placed += gcost[target]
                 target += 1
-            half = (gi + target) // 2
-            while gi < half:
-                for x in groups[gi]:
-                    sch.emit(x)
-                gi += 1
+            # the gap's LDS reads first: their data returns while its vector
+            # ops issue (reads after half or all of them: 6 % slower steps)
             sch.issue_reads()
             while gi < target:
                 for x in groups[gi]:
