@@ -381,8 +381,8 @@ class BK64:
         return res
 
     def run(self, sch, mfmas, slots, side, stfrag=None):
-        """Emits mfmas; after matrix instruction i its side ops, then half of
-        slots[i], then paced LDS reads, then the rest. Slot -1 comes before the
+        """Emits mfmas; after matrix instruction i its side ops, then the
+        paced LDS reads, then slots[i]. Slot -1 comes before the
         first matrix instruction. A side op "ADDR_TC" emits the transposed
         addresses of tile t (the caller's addr_tc) once every older
         transposed read has been issued."""
@@ -421,12 +421,9 @@ class BK64:
             sch.mfma(text, frags)
             for x in side.get(i, []):
                 put_side(x)
-            ops = slots.get(i, [])
-            h = 0  # the gap's LDS reads before its vector ops
-            for op in ops[:h]:
-                put(op)
+            # the gap's LDS reads first: their data returns while its vector ops issue
             sch.issue_reads()
-            for op in ops[h:]:
+            for op in slots.get(i, []):
                 put(op)
 
     PREF_KEEP = 8

@@ -298,8 +298,8 @@ class BQ64:
         return res
 
     def run(self, sch, mfmas, slots, side):
-        """Emits mfmas; after matrix instruction i its side ops, then half of
-        slots[i], then paced LDS reads, then the rest. Slot -1 comes before the
+        """Emits mfmas; after matrix instruction i its side ops, then the
+        paced LDS reads, then slots[i]. Slot -1 comes before the
         first matrix instruction. A side op ("ADDR_TC", old, ops) emits ops
         (the transposed addresses of tile t) once every older transposed read
         has been issued."""
@@ -336,12 +336,9 @@ class BQ64:
             sch.mfma(text, frags)
             for x in side.get(i, []):
                 put_side(x)
-            ops = slots.get(i, [])
-            h = 0  # the gap's LDS reads before its vector ops
-            for op in ops[:h]:
-                put(op)
+            # the gap's LDS reads first: their data returns while its vector ops issue
             sch.issue_reads()
-            for op in ops[h:]:
+            for op in slots.get(i, []):
                 put(op)
 
     PREF_KEEP = 4

@@ -396,8 +396,8 @@ class K32:
         return res
 
     def run(self, sch, mfmas, slots, side, stfrag=None):
-        """Emits mfmas; after matrix instruction i its side ops, then half of
-        slots[i], then paced LDS reads, then the rest. Slot -1 comes before the
+        """Emits mfmas; after matrix instruction i its side ops, then the
+        paced LDS reads, then slots[i]. Slot -1 comes before the
         first matrix instruction."""
         def put(op):
             if op == "WAIT_STATS":
@@ -425,12 +425,9 @@ class K32:
             sch.mfma(text, frags)
             for x in side.get(i, []):
                 sch.emit(x)
-            ops = slots.get(i, [])
-            h = 0  # the gap's LDS reads before its vector ops
-            for op in ops[:h]:
-                put(op)
+            # the gap's LDS reads first: their data returns while its vector ops issue
             sch.issue_reads()
-            for op in ops[h:]:
+            for op in slots.get(i, []):
                 put(op)
 
     def merge(self, *maps):
@@ -578,12 +575,9 @@ class K32:
                             sch.emit(y)
                     else:
                         sch.emit(x)
-                ops = slots.get(i, [])
-                h = 0  # the gap's LDS reads before its vector ops
-                for op in ops[:h]:
-                    put(op)
+                # the gap's LDS reads first: their data returns while its vector ops issue
                 sch.issue_reads()
-                for op in ops[h:]:
+                for op in slots.get(i, []):
                     put(op)
 
         def put(op):
